@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-sparse attention hot path on one MI355X.
+
+Headline (BASELINE.json `metric`, config 2): block-sparse prefill TFLOP/s on
+computed tiles at N = 8192 — bf16, H = 32, D = 128, route block 128, causal,
+tree-routed lists (p = 4 depth 3, LCA depth >= 2, + diagonal + sink). One
+step = sync-free block-list build + prefill forward over those lists, inputs
+resident in HBM. `value` = FLOP_alg / step time, FLOP_alg = 4 * D * 128^2 *
+sum(counts) (every listed 128x128 tile counted in full).
+
+Also reported: the prefill kernel alone (HIP events around back-to-back
+launches on its stream; `roofline` is built from it), the list build alone,
+sparse paged decode on config 4 (GB/s of routed KV bytes), and a CPU
+baseline: the fp32 masked-dense reference (oracle) on the host cores on a
+bounded sample of heads.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+Only one GPU is supported: --gpus N > 1 exits with a message.
+"""
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "sparse-ai_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
+    ap.add_argument("--cpu-heads", type=int, default=4, help="heads timed for the CPU baseline")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(fn, reps, torch):
+    """Average GPU time per call of `fn` over `reps` back-to-back calls (HIP events on
+    torch's current stream, which is where the kernels are launched)."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE {world}).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import sparse_workloads as wl
+    from ultrametric import block_list_attention, build_block_lists, ultrametric_decode
+    from ultrametric import _native as nat
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(2)
+    if not nat.available():
+        raise RuntimeError("libsparseattn.so is not built")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---------------- config 2: build + prefill -------------------------------------
+    log("generating config 2")
+    c = wl.config2(device=dev)
+    q, k, v, router = c["q"], c["k"], c["v"], c["router"]
+    Z, H, N, D = q.shape
+    RB = c["route_block"]
+
+    def build():
+        return build_block_lists(router, 2, is_causal=True, sink_block=True, arity=4)
+
+    bl = build()
+    counts = bl.counts
+    flop_alg = wl.prefill_flops(counts, D, RB)
+    n_tiles = int(counts.sum())
+    total_tiles = Z * H * (N // RB) ** 2
+    causal_tiles = Z * H * (N // RB) * (N // RB + 1) // 2
+    mask = wl.lists_to_block_mask(bl.lists, counts)
+    useful = wl.useful_prefill_flops(mask, RB, N, D, True)
+
+    def step():
+        b = build()
+        return block_list_attention(q, k, v, b, route_block=RB, is_causal=True)
+
+    with torch.no_grad():
+        log(f"warmup {args.warmup}")
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        s.record()
+        for _ in range(args.steps):
+            step()
+        e.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_step = s.elapsed_time(e) / args.steps
+        log(f"timed {args.steps} steps: {ms_step * 1e3:.1f} us/step (wall {wall * 1e3 / args.steps * 1e3:.1f} us)")
+
+        # prefill kernel alone (lists prebuilt), raw ABI launches back to back
+        out = torch.empty_like(q)
+        lists = bl.lists.contiguous()
+        st = [nat.strides(t) for t in (q, k, v, out)]
+        lib = nat.lib()
+        scale = 1.0 / math.sqrt(D)
+        stream = nat.stream(dev)
+
+        def fwd():
+            nat.check(lib.sa_block_sparse_fwd(nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), None,
+                                              nat.ptr(lists), nat.ptr(counts), None, 0, Z, H, H, N, D, RB,
+                                              bl.max_count, st[0], st[1], st[2], st[3], None, scale, 1, 1,
+                                              stream))
+
+        reps = max(50, args.steps)
+        fwd_ms = time_launches(fwd, reps, torch)
+        build_ms = time_launches(build, reps, torch)
+        ref_out = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True)
+        assert torch.equal(out, ref_out), "raw-ABI launch disagrees with the public API"
+    log(f"prefill kernel {fwd_ms * 1e3:.1f} us, build {build_ms * 1e3:.1f} us")
+
+    value = flop_alg / (ms_step * 1e-3) / 1e12
+    achieved = flop_alg / (fwd_ms * 1e-3) / 1e12
+    result = {
+        "metric": "block-sparse prefill TFLOP/s (computed tiles) at N=8K",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, seeded tree routing)",
+        "config": {
+            "workload": "config2: block-sparse prefill fwd, B1 H32 N8192 D128, route block 128, causal, "
+                        "p=4 depth-3 tree routing (LCA>=2) + diagonal + sink; step = sync-free list build + fwd",
+            "global_batch": 1, "seq_len": N, "heads": H, "head_dim": D, "route_block": RB,
+            "active_tiles": n_tiles, "tile_density_full": round(n_tiles / total_tiles, 5),
+            "tile_density_causal": round(n_tiles / causal_tiles, 5),
+            "flop_alg": flop_alg, "flop_useful_token_exact": useful,
+            "parallelism": "single GPU",
+        },
+        "prefill_kernel_ms": round(fwd_ms, 5),
+        "build_ms": round(build_ms, 5),
+        "roofline": {
+            "kernel": "prefill_mfma_kernel<bf16,128,4,64,causal>",
+            "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "unique_hbm_bytes": 4 * q.numel() * q.element_size(),
+        },
+    }
+
+    # ---------------- config 4: sparse paged decode -----------------------------------
+    if not args.no_decode:
+        log("generating config 4")
+        w = wl.config4(device=dev)
+        kw = dict(req_depth=w.req_depth, local_blocks=w.local_blocks, sink_block=w.sink_block)
+        b_alg, upages = wl.decode_routed_bytes(w)
+        ws = torch.empty(nat.lib().sa_decode_workspace_bytes(64, 32, 128, w.block_tables.shape[1]),
+                         dtype=torch.uint8, device=dev)
+
+        def dec():
+            return ultrametric_decode(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.router,
+                                      w.q_router, workspace=ws, **kw)
+
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                dec()
+            dec_ms = time_launches(dec, max(50, args.steps), torch)
+        meta_bytes = int(w.context_lens.add(15).div(16, rounding_mode="floor").sum()) * (4 + 32 * 4 * 4)
+        dec_gbs = b_alg / (dec_ms * 1e-3) / 1e9
+        result["decode"] = {
+            "workload": "config4: 64 seqs, L~U[4096,32768], GQA 32/8, D128, page 16, p=4 depth-4 routing "
+                        "(req_depth 4) + sink + last 4 pages, bf16",
+            "ms_per_call": round(dec_ms, 5),
+            "routed_kv_bytes": b_alg, "unique_pages": upages,
+            "routing_metadata_bytes": meta_bytes,
+            "gbs_routed": round(dec_gbs, 1),
+            "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(dec_gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        }
+        log(f"decode {dec_ms * 1e3:.1f} us/call, {dec_gbs:.0f} GB/s on routed bytes")
+        del w
+
+    # ---------------- CPU baseline (oracle, host cores) --------------------------------
+    if not args.no_cpu:
+        from oracle import attention as oa
+        heads = list(range(min(args.cpu_heads, H)))
+        qc, kc, vc = (t[0, heads].cpu() for t in (q, k, v))
+        mk = mask[0, heads].cpu()
+        oa.masked_attention_torch_fp32(qc[:1, :256], kc[:1, :256], vc[:1, :256], mk[:1, :2, :2], RB, True)
+        t0 = time.perf_counter()
+        oa.masked_attention_torch_fp32(qc, kc, vc, mk, RB, True)
+        cpu_s = time.perf_counter() - t0
+        flop_sample = wl.prefill_flops(counts[0, heads], D, RB)
+        result["cpu_baseline"] = {
+            "value": round(flop_sample / cpu_s / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"fp32 masked-dense oracle (oracle/attention.py masked_attention_torch_fp32) on "
+                      f"{len(heads)} of {H} heads of config 2, query-chunked 2048; {cpu_s:.2f} s; "
+                      f"FLOP_alg of those heads' listed tiles / wall time",
+            "cpu_model": platform.processor() or platform.machine(),
+            "os_cpu_count": os.cpu_count(),
+        }
+        log(f"cpu baseline {cpu_s:.2f} s for {len(heads)} heads")
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

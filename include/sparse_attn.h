@@ -1,0 +1,175 @@
+/*
+ * sparse_attn.h — C ABI of libsparseattn.so, the MI355X (gfx950) block-sparse
+ * attention hot path: block-list compaction, block-sparse prefill forward and
+ * sparse paged decode.
+ *
+ * The reference (sparse-ai, src/ultrametric) has no C ABI: its boundary is a
+ * Python function API backed by Triton kernels. Each entry point below names
+ * the Python function / Triton kernel it replaces; the Python package
+ * `ultrametric` in this repository keeps those Python names and calls these
+ * functions through ctypes.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are DEVICE pointers (HIP, gfx950). Strides are in
+ *     elements, not bytes. Nothing here allocates device memory; callers pass
+ *     outputs and any workspace.
+ *   - Every call is asynchronous on `stream` (a hipStream_t passed as void*;
+ *     NULL = the legacy default stream) and performs no host<->device sync.
+ *   - Return value: SA_OK (0) on success, a negative SA_E* code otherwise;
+ *     sa_last_error() then returns a thread-local message. Argument errors are
+ *     detected on the host before any launch.
+ *   - Calls are reentrant; the library keeps no global mutable state apart
+ *     from the thread-local error string.
+ */
+#ifndef SPARSE_ATTN_H
+#define SPARSE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_ABI_VERSION 1
+
+/* Status codes. */
+#define SA_OK 0
+#define SA_EINVAL (-1)        /* bad shape / stride / parameter (Python: ValueError) */
+#define SA_EUNSUPPORTED (-2)  /* valid but not implemented here (Python: RuntimeError) */
+#define SA_ELAUNCH (-3)       /* HIP launch or runtime error (Python: RuntimeError) */
+
+/* Element types. */
+#define SA_DTYPE_F32 0
+#define SA_DTYPE_BF16 1
+#define SA_DTYPE_F16 2
+#define SA_DTYPE_I32 3
+#define SA_DTYPE_I64 4
+#define SA_DTYPE_U8 5  /* bool masks */
+
+/* ABI version of the loaded library (SA_ABI_VERSION it was built with). */
+int sa_abi_version(void);
+
+/* Thread-local message describing the last failed call on this thread. */
+const char* sa_last_error(void);
+
+/*
+ * Block-list compaction from per-block routing vectors.
+ * Replaces: build_block_lists() and _build_block_lists_kernel
+ *   (src/ultrametric/block_list.py:170-278 and :127-167).
+ *
+ * router      (Z, H, NB, TD) integer branch ids, element type router_dtype
+ *             (SA_DTYPE_I32 or SA_DTYPE_I64), strides router_strides[4].
+ * depth_dev   optional (H,) int64 device array of per-head required depths;
+ *             when NULL every head uses depth_uniform. Depths must already be
+ *             validated to lie in [0, TD] (block_list.py:93-104).
+ * base        mixed-radix base (block_list.py:211-215): max(2, arity) in the
+ *             sync-free mode, max(2, max(id)+1) otherwise.
+ * use_codes   1: blocks match iff their mixed-radix codes
+ *             sum_l id_l * [l < depth] * base^l (int64, wrapping) are equal
+ *             (block_list.py:224-229); 0: element-wise equality on the first
+ *             depth levels (block_list.py:256-258). The reference picks 1 iff
+ *             TD * log2(base) < 62.
+ * is_causal / sink_block / local_blocks: structural masks applied in the
+ *             reference order: local band OR, sink column OR, causal AND
+ *             (block_list.py:107-118).
+ * lists       (Z, H, NB, lists_cols) int32 contiguous output, or NULL to
+ *             compute counts only. Row (z,h,i) receives its active key blocks
+ *             in ascending order, then zeros up to lists_cols. lists_cols must
+ *             be >= the largest count (NB in the sync-free mode).
+ * counts      (Z, H, NB) int32 contiguous output.
+ * Limits: NB <= 8192.
+ */
+int sa_build_block_lists(const void* router, int router_dtype, const int64_t* router_strides,
+                         int Z, int H, int NB, int TD, const int64_t* depth_dev, int depth_uniform,
+                         int64_t base, int use_codes, int is_causal, int sink_block,
+                         int local_blocks, int32_t* lists, int lists_cols, int32_t* counts,
+                         void* stream);
+
+/*
+ * Block-list compaction from an explicit per-head block mask.
+ * Replaces: the compaction step of build_block_lists applied to a given
+ *   `match` (src/ultrametric/block_list.py:263-278); extension named by the
+ *   hot-path scope (block mask -> block list).
+ *
+ * mask        (Z, H, NB, NB) uint8 (non-zero = active), strides mask_strides[4].
+ * The structural masks are applied on top, in the same order as above.
+ * lists / lists_cols / counts as for sa_build_block_lists.
+ */
+int sa_build_block_lists_mask(const uint8_t* mask, const int64_t* mask_strides, int Z, int H,
+                              int NB, int is_causal, int sink_block, int local_blocks,
+                              int32_t* lists, int lists_cols, int32_t* counts, void* stream);
+
+/*
+ * Block-sparse attention forward over block lists.
+ * Replaces: _block_list_attention_fwd / _block_list_fwd_kernel
+ *   (src/ultrametric/block_list.py:688-757 and :387-470).
+ *
+ * q, out      (Z, H, N, D); k, v (Z, H_kv, N, D) with H % H_kv == 0 (GQA:
+ *             query head h reads kv head h / (H / H_kv)). Element type dtype
+ *             (SA_DTYPE_F32 / SA_DTYPE_BF16 / SA_DTYPE_F16) for all four.
+ *             Strides q_strides[4], k_strides[4], v_strides[4], o_strides[4].
+ * lse         optional (Z, H, N) fp32 contiguous output: natural-log
+ *             log-sum-exp of the scaled scores, -inf for rows with no key.
+ * lists       (Z, H, NB, max_count) int32 contiguous, NB = ceil(N/route_block);
+ * counts      (Z, H, NB) int32 contiguous. Only the first counts[row] entries
+ *             of a row are read; each must lie in [0, NB).
+ * soft_bias   optional (Z, H, NB, max_count) additive logit bias per listed
+ *             block, element type soft_bias_dtype (F32/BF16/F16), strides
+ *             sb_strides[4].
+ * route_block power of two >= 16; D power of two in [16, 256].
+ * Rows of out with index >= N are never written; out = 0 for rows with no
+ * visible key.
+ */
+int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                        const int32_t* lists, const int32_t* counts, const void* soft_bias,
+                        int soft_bias_dtype, int Z, int H, int H_kv, int N, int D,
+                        int route_block, int max_count, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides,
+                        const int64_t* o_strides, const int64_t* sb_strides, float sm_scale,
+                        int dtype, int is_causal, void* stream);
+
+/*
+ * Workspace bytes needed by sa_sparse_paged_decode for B sequences of H query
+ * heads of dimension D with at most max_pages logical pages each.
+ * No reference counterpart (the reference decode keeps no split-KV partials).
+ */
+size_t sa_decode_workspace_bytes(int B, int H, int D, int max_pages);
+
+/*
+ * Sparse paged decode with tree-routed page selection.
+ * Replaces: ultrametric_decode / _ultrametric_decode_kernel
+ *   (src/ultrametric/kernel_decode.py:188-247 and :22-124), with the CPU
+ *   reference semantics for ctx_len <= 0 (zeros, kernel_decode.py:145-152)
+ *   and GQA added (k/v caches carry H_kv heads, H % H_kv == 0).
+ *
+ * q           (B, H, D); out (B, H, D) — dtype, strides q_strides[3] / o_strides[3].
+ * k_cache, v_cache (P, H_kv, page, D) — dtype, strides k_strides[4] / v_strides[4].
+ * block_tables (B, max_pages) int32, strides bt_strides[2]: logical -> physical page.
+ * context_lens (B,) int32 contiguous.
+ * router      (P, H, TD) int32, strides r_strides[3]: routing vector per
+ *             (physical page, query head).
+ * q_router    (B, H, TD) int32, strides qr_strides[3].
+ * req_depth   levels that must agree (clamped to [0, TD]).
+ * A logical page l of sequence b is attended by head h iff its routing
+ * vector matches on the first req_depth levels, or (sink_block and l == 0),
+ * or (local_blocks > 0 and l >= n_pages - local_blocks). Tokens >= ctx_len
+ * are masked; scale = 1/sqrt(D); heads with no selected page get zeros.
+ * workspace   device buffer of at least sa_decode_workspace_bytes(...) bytes.
+ */
+int sa_sparse_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* block_tables, const int32_t* context_lens,
+                           const int32_t* router, const int32_t* q_router, void* out, int B,
+                           int H, int H_kv, int D, int page_size, int TD, int max_pages,
+                           int num_phys_pages, int req_depth, int local_blocks, int sink_block,
+                           const int64_t* q_strides, const int64_t* k_strides,
+                           const int64_t* v_strides, const int64_t* bt_strides,
+                           const int64_t* r_strides, const int64_t* qr_strides,
+                           const int64_t* o_strides, void* workspace, size_t workspace_bytes,
+                           int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSE_ATTN_H */

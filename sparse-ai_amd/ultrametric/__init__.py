@@ -1,0 +1,35 @@
+"""ultrametric — MI355X-native block-sparse attention hot path of sparse-ai.
+
+Drop-in for the kernel API of the reference package ``src/ultrametric``
+(__init__.py:24-36 and kernel_decode.py): the same function names and
+signatures, backed by hand-written HIP kernels for gfx950 in libsparseattn.so.
+The reference's training model, topology routers, layers and legacy kernels
+are outside this package's scope.
+"""
+
+from .block_list import (
+    HAS_HIP,
+    HAS_TRITON,
+    BlockLists,
+    block_list_attention,
+    block_lists_from_mask,
+    build_block_lists,
+    build_transposed_block_lists,
+    routed_block_attention,
+)
+from .kernel import block_sparse_attention, routing_to_block_indices
+from .kernel_decode import ultrametric_decode
+
+__all__ = [
+    "HAS_TRITON",
+    "HAS_HIP",
+    "BlockLists",
+    "build_block_lists",
+    "block_lists_from_mask",
+    "build_transposed_block_lists",
+    "block_list_attention",
+    "routed_block_attention",
+    "block_sparse_attention",
+    "routing_to_block_indices",
+    "ultrametric_decode",
+]

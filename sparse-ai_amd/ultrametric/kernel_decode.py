@@ -1,0 +1,132 @@
+"""Sparse paged decode on MI355X (drop-in for src/ultrametric/kernel_decode.py).
+
+``ultrametric_decode`` keeps the reference signature (kernel_decode.py:188-199)
+and runs the HIP split-KV decode kernels of libsparseattn.so on torch's
+current stream. Extensions: GQA (k_cache / v_cache may carry H_kv | H heads;
+query head h reads kv head h // (H / H_kv)); ``context_lens <= 0`` yields
+zeros, as the reference's CPU reference does (kernel_decode.py:145-147).
+Block-table entries outside [0, num_pages) are treated as unselected pages
+and logical pages beyond block_tables.shape[1] are ignored (memory safety).
+
+``_ultrametric_decode_reference`` keeps the reference's torch loop
+(kernel_decode.py:129-185) for callers' checks; ``ultrametric_decode`` never
+calls it and has no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+
+HAS_TRITON = nat.available()
+
+__all__ = ["HAS_TRITON", "ultrametric_decode", "_ultrametric_decode_reference", "decode_workspace_bytes"]
+
+
+def decode_workspace_bytes(batch_size: int, num_heads: int, head_dim: int, max_pages: int) -> int:
+    """Bytes of split-KV scratch the decode kernels need."""
+    return int(nat.lib().sa_decode_workspace_bytes(batch_size, num_heads, head_dim, max_pages))
+
+
+def ultrametric_decode(
+    q,
+    k_cache,
+    v_cache,
+    block_tables,
+    context_lens,
+    router_indices,
+    q_router_indices,
+    req_depth,
+    local_blocks: int = 0,
+    sink_block: bool = False,
+    workspace: torch.Tensor = None,
+):
+    """Decode one query token per sequence against routed KV pages.
+
+    q: (B, H, D); k_cache, v_cache: (num_pages, H_kv, page_size, D);
+    block_tables: (B, max_pages) int; context_lens: (B,) int;
+    router_indices: (num_pages, H, TD) int; q_router_indices: (B, H, TD) int.
+    ``workspace`` (optional, uint8, >= decode_workspace_bytes(...)) avoids a
+    per-call allocation. Returns (B, H, D) in q.dtype.
+    """
+    batch_size, num_heads, head_dim = q.shape
+    tree_depth = int(q_router_indices.shape[-1])
+    assert tree_depth >= 1, "tree_depth must be >= 1"
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError(f"k_cache / v_cache must be (pages, H_kv, page, D); got {tuple(k_cache.shape)}, "
+                         f"{tuple(v_cache.shape)}")
+    if k_cache.shape[3] != head_dim or num_heads % k_cache.shape[1] != 0:
+        raise ValueError("k_cache head_dim / head count incompatible with q")
+    if not (q.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("q, k_cache, v_cache must share dtype")
+    dev = nat.require_device(q, k_cache, v_cache, block_tables, context_lens, router_indices,
+                             q_router_indices)
+    if k_cache.stride(3) != 1:
+        k_cache = k_cache.contiguous()
+    if v_cache.stride(3) != 1:
+        v_cache = v_cache.contiguous()
+    bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+    ctx = context_lens.to(torch.int32).contiguous()
+    rt = router_indices if router_indices.dtype == torch.int32 else router_indices.to(torch.int32)
+    qrt = q_router_indices if q_router_indices.dtype == torch.int32 else q_router_indices.to(torch.int32)
+    num_pages, H_kv, page_size, _ = k_cache.shape
+    max_pages = bt.shape[1]
+    out = torch.empty((batch_size, num_heads, head_dim), dtype=q.dtype, device=dev)
+    need = decode_workspace_bytes(batch_size, num_heads, head_dim, max_pages)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    dt = nat.dtype_code(q.dtype, (torch.float32, torch.bfloat16, torch.float16))
+    lib = nat.lib()
+    with torch.cuda.device(dev):
+        rc = lib.sa_sparse_paged_decode(
+            nat.ptr(q), nat.ptr(k_cache), nat.ptr(v_cache), nat.ptr(bt), nat.ptr(ctx), nat.ptr(rt),
+            nat.ptr(qrt), nat.ptr(out), batch_size, num_heads, H_kv, head_dim, page_size, tree_depth,
+            max_pages, num_pages, int(req_depth), int(local_blocks), int(bool(sink_block)),
+            nat.strides(q), nat.strides(k_cache), nat.strides(v_cache), nat.strides(bt),
+            nat.strides(rt), nat.strides(qrt), nat.strides(out), nat.ptr(workspace),
+            workspace.numel(), dt, nat.stream(dev))
+    nat.check(rc)
+    return out
+
+
+def _ultrametric_decode_reference(q, k_cache, v_cache, block_tables, context_lens, router_indices,
+                                  q_router_indices, req_depth, local_blocks: int = 0,
+                                  sink_block: bool = False):
+    """The reference's torch loop (kernel_decode.py:129-185), GQA by head grouping."""
+    batch_size, num_heads, head_dim = q.shape
+    group = num_heads // k_cache.shape[1]
+    tree_depth = q_router_indices.shape[-1]
+    r = min(max(int(req_depth), 0), tree_depth)
+    block_size = k_cache.shape[2]
+    sm_scale = 1.0 / (head_dim ** 0.5)
+    out = torch.zeros_like(q)
+    for b in range(batch_size):
+        ctx_len = int(context_lens[b].item())
+        if ctx_len <= 0:
+            continue
+        num_logical = (ctx_len + block_size - 1) // block_size
+        phys_ids = block_tables[b, :num_logical].long()
+        for h in range(num_heads):
+            q_vec = q[b, h].float()
+            if r > 0:
+                match = (router_indices[phys_ids, h, :r] == q_router_indices[b, h, :r].unsqueeze(0)).all(dim=-1)
+            else:
+                match = torch.ones(num_logical, dtype=torch.bool, device=q.device)
+            if sink_block and num_logical > 0:
+                match[0] = True
+            if local_blocks > 0:
+                match[max(0, num_logical - local_blocks):] = True
+            if not match.any():
+                continue
+            k_sel, v_sel = [], []
+            for l_idx in range(num_logical):
+                if not match[l_idx]:
+                    continue
+                p_idx = int(phys_ids[l_idx].item())
+                valid = min(block_size, ctx_len - l_idx * block_size)
+                k_sel.append(k_cache[p_idx, h // group, :valid].float())
+                v_sel.append(v_cache[p_idx, h // group, :valid].float())
+            scores = torch.matmul(torch.cat(k_sel, 0), q_vec) * sm_scale
+            out[b, h] = torch.matmul(torch.softmax(scores, dim=-1), torch.cat(v_sel, 0)).to(q.dtype)
+    return out

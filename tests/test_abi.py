@@ -1,0 +1,102 @@
+"""C-ABI library checks that need no GPU: it loads, exports every symbol that
+include/sparse_attn.h declares, reports its ABI version, and rejects bad
+arguments on the host with the documented status codes. The Python layer
+raises instead of falling back to the CPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from ultrametric import _native as nat
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sparse_attn.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(sa_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_header_symbols():
+    assert os.path.exists(nat.LIB_PATH), "build libsparseattn.so first (__graft_entry__.build())"
+    lib = ctypes.CDLL(nat.LIB_PATH)
+    syms = declared_symbols()
+    assert len(syms) >= 7
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert set(syms) == set(nat.EXPORTED_SYMBOLS)
+    assert nat.lib().sa_abi_version() == 1
+
+
+def test_host_side_argument_errors():
+    lib = nat.lib()
+    st = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    # NULL router
+    rc = lib.sa_build_block_lists(None, 3, st, 1, 1, 4, 2, None, 1, 2, 1, 0, 0, 0, None, 4, None, None)
+    assert rc == nat.SA_EINVAL and b"NULL" in lib.sa_last_error()
+    # bad router dtype
+    rc = lib.sa_build_block_lists(ctypes.c_void_p(16), 0, st, 1, 1, 4, 2, None, 1, 2, 1, 0, 0, 0, None, 4,
+                                  ctypes.c_void_p(16), None)
+    assert rc == nat.SA_EINVAL
+    # depth out of range
+    rc = lib.sa_build_block_lists(ctypes.c_void_p(16), 3, st, 1, 1, 4, 2, None, 3, 2, 1, 0, 0, 0, None, 4,
+                                  ctypes.c_void_p(16), None)
+    assert rc == nat.SA_EINVAL
+    # NB beyond the LDS code table
+    rc = lib.sa_build_block_lists(ctypes.c_void_p(16), 3, st, 1, 1, 9000, 2, None, 1, 2, 1, 0, 0, 0, None, 4,
+                                  ctypes.c_void_p(16), None)
+    assert rc == nat.SA_EUNSUPPORTED
+    # forward: head_dim not a power of two, route block too small, D too large
+    p = ctypes.c_void_p(256)
+    for D, rb, code in ((48, 64, nat.SA_EINVAL), (64, 8, nat.SA_EINVAL), (512, 64, nat.SA_EUNSUPPORTED)):
+        rc = lib.sa_block_sparse_fwd(p, p, p, p, None, p, p, None, 0, 1, 1, 1, 64, D, rb, 1, st, st, st, st,
+                                     None, 0.1, 1, 0, None)
+        assert rc == code, (D, rb)
+    # decode: unsupported GQA group, too small workspace
+    st3 = (ctypes.c_int64 * 3)(1, 1, 1)
+    st2 = (ctypes.c_int64 * 2)(1, 1)
+    stk = (ctypes.c_int64 * 4)(2 * 16 * 64, 16 * 64, 64, 1)
+    args = [p] * 8 + [1, 6, 2, 64, 16, 4, 4, 10, 4, 0, 0, st3, stk, stk, st2, st3, st3, st3, p, 0, 1, None]
+    assert lib.sa_sparse_paged_decode(*args) == nat.SA_EUNSUPPORTED
+    args[9] = 8
+    assert lib.sa_sparse_paged_decode(*args) == nat.SA_EINVAL
+    assert b"workspace" in lib.sa_last_error()
+    assert lib.sa_decode_workspace_bytes(2, 8, 64, 300) == 2 * 8 * 2 * 66 * 4
+
+
+def test_python_layer_raises_on_cpu_tensors():
+    from ultrametric import block_list_attention, build_block_lists, ultrametric_decode
+    r = torch.zeros(1, 1, 4, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="HIP"):
+        build_block_lists(r, 1, arity=2)
+    q = torch.zeros(1, 1, 64, 32)
+    bl = (torch.zeros(1, 1, 1, 1, dtype=torch.int32), torch.ones(1, 1, 1, dtype=torch.int32), 1)
+    with pytest.raises(RuntimeError, match="HIP"):
+        block_list_attention(q, q, q, bl, route_block=64)
+    with pytest.raises(RuntimeError, match="HIP"):
+        ultrametric_decode(torch.zeros(1, 1, 16), torch.zeros(1, 1, 4, 16), torch.zeros(1, 1, 4, 16),
+                           torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32),
+                           torch.zeros(1, 1, 2, dtype=torch.int32), torch.zeros(1, 1, 2, dtype=torch.int32), 1)
+
+
+def test_python_validation_matches_reference_errors():
+    from ultrametric import block_list_attention, build_block_lists
+    with pytest.raises(ValueError):
+        build_block_lists(torch.zeros(2, 3, 4, dtype=torch.int32), 1)          # not 4-D
+    with pytest.raises(ValueError):
+        build_block_lists(torch.zeros(1, 2, 4, 3, dtype=torch.int32), 4, arity=2)
+    q = torch.zeros(1, 2, 64, 48)
+    bl = (torch.zeros(1, 2, 1, 1, dtype=torch.int32), torch.ones(1, 2, 1, dtype=torch.int32), 1)
+    with pytest.raises(ValueError, match="head_dim"):
+        block_list_attention(q, q, q, bl, route_block=64)
+    q = torch.zeros(1, 2, 64, 32)
+    with pytest.raises(ValueError, match="route_block"):
+        block_list_attention(q, q, q, bl, route_block=48)
+    with pytest.raises(ValueError, match="block_lists built for"):
+        block_list_attention(q, q, q, bl, route_block=32)
+    with pytest.raises(ValueError, match="divide"):
+        block_list_attention(q, q, q, bl, route_block=64, block_m=48)
