@@ -75,6 +75,8 @@ template <> __device__ __forceinline__ float round_to<f16_t>(float x) {
   return f16_bits_to_float(float_to_f16_bits(x));
 }
 
+constexpr int kListCache = 1024;  // MFMA path: a row's list (<= 1024 blocks) lives in LDS
+
 // XCD-aware work index: workgroup b runs on XCD b % 8; give each XCD a
 // contiguous range of the T work items.
 __device__ __forceinline__ int xcd_remap(int b, int T) {
@@ -187,9 +189,7 @@ template <> struct Mma<bf16_t> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(vec, a),
                                                    __builtin_bit_cast(vec, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
-    return float_to_bf16_bits(lo) | (float_to_bf16_bits(hi) << 16);
-  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
 };
 template <> struct Mma<f16_t> {
   typedef f16x8_t vec;
@@ -197,13 +197,12 @@ template <> struct Mma<f16_t> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(vec, a),
                                                   __builtin_bit_cast(vec, b), c, 0, 0, 0);
   }
-  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
-    return float_to_f16_bits(lo) | (float_to_f16_bits(hi) << 16);
-  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
 };
 
 template <typename T, int D, int NW, int BN, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_mfma_kernel(FwdParams p) {
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;
   constexpr int CPR = D / 8;   // 16-byte chunks per row
@@ -219,6 +218,10 @@ __global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
 
   __shared__ u32x4_t k_lds[2][K_CHUNKS];
   __shared__ u32x2_t v_lds[2][NQ * D];
+  // The row's list (and soft biases) staged once: reading them from LDS in
+  // the loop keeps global loads out of the way of the K/V prefetch.
+  __shared__ int32_t list_lds[kListCache];
+  __shared__ float bias_lds[kListCache];
 
   const int work = xcd_remap(blockIdx.x, p.total_wg);
   const int zh = work / p.mtiles;
@@ -234,6 +237,11 @@ __global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
+  for (int t = tid; t < count; t += NT) {
+    list_lds[t] = list[t];
+    if (p.sb) bias_lds[t] = load_bias(p, z, h, qb, t);
+  }
+  __syncthreads();
   const int li = lane & 31, kh = lane >> 5;
   const int qw0 = m0 + wave * 32;
   const int qpos = qw0 + li;
@@ -245,11 +253,13 @@ __global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
 
   // Q^T operand, resident for the whole row: lane (li + 32 kh) holds
   // Q[qpos][16 s + 8 kh .. +8].
+  // Rows past N are clamped to row N-1 (never stored): every load is
+  // unconditional, so the compiler can count outstanding loads exactly.
   u32x4_t qf[KS];
+  const int qrow = qpos < N ? qpos : N - 1;
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    qf[s] = qpos < N ? *reinterpret_cast<const u32x4_t*>(qp + qpos * p.qs2 + 16 * s + 8 * kh)
-                     : u32x4_t{0u, 0u, 0u, 0u};
+    qf[s] = *reinterpret_cast<const u32x4_t*>(qp + qrow * p.qs2 + 16 * s + 8 * kh);
   }
 
   f32x16_t acc[DT];
@@ -260,29 +270,30 @@ __global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
   u32x4_t kreg[KPT];
   u32x4_t vreg[VPT][4];
 
-  auto tile_key0 = [&](int n) { return list[n / spb] * p.RB + (n % spb) * BN; };
+  auto tile_key0 = [&](int n) { return list_lds[n / spb] * p.RB + (n % spb) * BN; };
 
+  // Keys outside [0, N) load row 0 instead (branch-free, always in bounds):
+  // their scores are masked to -inf, so p = 0 exactly and the finite data
+  // they bring never reaches the output.
+  auto clamp_key = [&](int key) { return static_cast<unsigned>(key) < static_cast<unsigned>(N) ? key : 0; };
   auto load_tile = [&](int n) {
     const int key0 = tile_key0(n);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int ci = tid + i * NT;
-      if (ci < K_CHUNKS) {
-        const int j = ci / CPR, c = ci % CPR, key = key0 + j;
-        kreg[i] = static_cast<unsigned>(key) < static_cast<unsigned>(N) ? *reinterpret_cast<const u32x4_t*>(kp + key * p.ks2 + 8 * c)
-                          : u32x4_t{0u, 0u, 0u, 0u};
+      if (K_CHUNKS % NT == 0 || ci < K_CHUNKS) {
+        const int j = ci / CPR, c = ci % CPR;
+        kreg[i] = *reinterpret_cast<const u32x4_t*>(kp + clamp_key(key0 + j) * p.ks2 + 8 * c);
       }
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int pi = tid + i * NT;
-      if (pi < V_PAIRS) {
+      if (V_PAIRS % NT == 0 || pi < V_PAIRS) {
         const int q4 = pi / CPR, c = pi % CPR;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = key0 + 4 * q4 + r;
-          vreg[i][r] = static_cast<unsigned>(key) < static_cast<unsigned>(N) ? *reinterpret_cast<const u32x4_t*>(vp + key * p.vs2 + 8 * c)
-                               : u32x4_t{0u, 0u, 0u, 0u};
+          vreg[i][r] = *reinterpret_cast<const u32x4_t*>(vp + clamp_key(key0 + 4 * q4 + r) * p.vs2 + 8 * c);
         }
       }
     }
@@ -292,7 +303,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int ci = tid + i * NT;
-      if (ci < K_CHUNKS) {
+      if (K_CHUNKS % NT == 0 || ci < K_CHUNKS) {
         const int j = ci / CPR, c = ci % CPR;
         k_lds[buf][j * CPR + (c ^ (j & (CPR - 1)))] = kreg[i];
       }
@@ -300,7 +311,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int pi = tid + i * NT;
-      if (pi < V_PAIRS) {
+      if (V_PAIRS % NT == 0 || pi < V_PAIRS) {
         const int q4 = pi / CPR, c = pi % CPR;
         // Entry for column 8c + e: the four keys' 16-bit values of that column.
         u32x2_t ent[8];
@@ -324,22 +335,27 @@ __global__ __launch_bounds__(NW * 64) void prefill_mfma_kernel(FwdParams p) {
     load_tile(0);
     store_tile(0);
   }
+  // Wait for every outstanding load (Q included) on all paths into the loop,
+  // so the loop's waits only ever cover its own prefetch.
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   int cur_t = -1;
   float bias = 0.f;
   for (int n = 0; n < total; ++n) {
     const int buf = n & 1;
+    // Everything this tile needs from memory other than LDS is read before
+    // the next tile's prefetch is issued (loads complete in order).
+    const int key0 = tile_key0(n);
+    const int t = n / spb;
+    if (p.sb && t != cur_t) {
+      bias = bias_lds[t];
+      cur_t = t;
+    }
     if (n + 1 < total) load_tile(n + 1);
 
-    const int key0 = tile_key0(n);
     const bool skip = qw0 >= N || static_cast<unsigned>(key0) >= static_cast<unsigned>(N) || (CAUSAL && key0 > qw0 + 31);
     if (!skip) {
-      const int t = n / spb;
-      if (p.sb && t != cur_t) {
-        bias = load_bias(p, z, h, qb, t);
-        cur_t = t;
-      }
       const bool need_mask = key0 + BN > N || (CAUSAL && key0 + BN - 1 > qw0);
 
       f32x16_t st[ST];
@@ -531,7 +547,7 @@ extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, 
                        p.qs0 % 8 == 0 && p.ks0 % 8 == 0 && p.vs0 % 8 == 0 && p.os0 % 8 == 0 &&
                        aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
   const bool mfma_ok = dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128) &&
-                       route_block >= 32 && rows_ok;
+                       route_block >= 32 && rows_ok && max_count <= kListCache;
   const long long wg = static_cast<long long>(Z) * H * ((N + 15) / 16);
   if (wg > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
 

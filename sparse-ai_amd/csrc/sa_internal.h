@@ -29,18 +29,26 @@ struct f16_t { uint16_t bits; };
 __device__ __forceinline__ float bf16_bits_to_float(uint32_t b) {
   return __uint_as_float(b << 16);
 }
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even conversions on gfx950's packed converters
+// (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), f16x2_t));
+}
 __device__ __forceinline__ uint32_t float_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 __device__ __forceinline__ float f16_bits_to_float(uint32_t b) {
-  return __half2float(__ushort_as_half(static_cast<unsigned short>(b)));
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
 }
 __device__ __forceinline__ uint32_t float_to_f16_bits(float f) {
-  return __half_as_ushort(__float2half_rn(f));
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
 template <typename T> struct Elem;
