@@ -43,6 +43,8 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--cpu-heads", type=int, default=4, help="heads timed for the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (reference for HBM byte counters)")
     return ap.parse_args()
 
 
@@ -179,6 +181,17 @@ def main():
             "unique_hbm_bytes": 4 * q.numel() * q.element_size(),
         },
     }
+
+    if args.calibrate_copy:
+        # A plain copy of known size: under `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE`
+        # its dispatch reads / writes exactly 256 MiB, which calibrates those counters.
+        src = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = src.numel() * src.element_size()
+        del src, dst
 
     # ---------------- config 4: sparse paged decode -----------------------------------
     if not args.no_decode:

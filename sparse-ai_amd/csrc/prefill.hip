@@ -26,6 +26,9 @@
 //    does not cover.
 #include "sa_internal.h"
 
+#include <algorithm>
+#include <type_traits>
+
 namespace sa {
 namespace {
 
@@ -200,26 +203,54 @@ template <> struct Mma<f16_t> {
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
 };
 
-template <typename T, int D, int NW, int BN, bool CAUSAL>
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt / lgkmcnt left at
+// their "no wait" maxima).
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(VM >= 0 && VM < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Workgroup barrier without the release/acquire fences of __syncthreads():
+// the fence would wait for every in-flight direct-to-LDS load of the
+// pipeline. The kernel orders its own LDS traffic with explicit waits.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+#define SA_LDS __attribute__((address_space(3)))
+
+// Direct-to-LDS load of 16 bytes per lane: lane L's bytes land at LDS
+// address lds_addr + 16 L. Issued through inline asm so that the compiler
+// does not track it: its own wait insertion would otherwise drain every
+// in-flight load before any LDS read. The kernel waits for these loads with
+// explicit vmcnt counts before the barrier that publishes a stage.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_addr), "v"(src) : "memory", "m0");
+}
+
+template <typename T, int D, int NW, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_mfma_kernel(FwdParams p) {
+  constexpr int BN = 32;               // keys per pipeline stage
+  constexpr int S = 4;                 // pipeline stages (tiles in flight: S - 1)
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;
-  constexpr int CPR = D / 8;   // 16-byte chunks per row
-  constexpr int KS = D / 16;   // MFMA k-steps of S^T = K Q^T
-  constexpr int ST = BN / 32;  // 32-key S^T tiles per sub-tile
-  constexpr int DT = D / 32;   // 32-row O^T tiles
-  constexpr int PS = BN / 16;  // MFMA k-steps of O^T += V^T P^T
-  constexpr int NQ = BN / 4;   // key quads per sub-tile
-  constexpr int K_CHUNKS = BN * CPR;
-  constexpr int V_PAIRS = NQ * CPR;
-  constexpr int KPT = (K_CHUNKS + NT - 1) / NT;
-  constexpr int VPT = (V_PAIRS + NT - 1) / NT;
+  constexpr int CPR = D / 8;           // 16-byte chunks per row
+  constexpr int ROWB = D * 2;          // bytes per K / V row
+  constexpr int TILEB = BN * ROWB;     // one K (or V) tile
+  constexpr int STAGEB = 2 * TILEB;    // K tile, then V tile
+  constexpr int KS = D / 16;           // MFMA k-steps of S^T = K Q^T
+  constexpr int DT = D / 32;           // 32-row O^T tiles
+  constexpr int NKI = TILEB / 1024;    // 1-KB direct-to-LDS loads per K tile
+  constexpr int LPW = 2 * NKI / NW;    // loads per wave per stage (K and V)
+  constexpr int RSH = D == 128 ? 0 : (D == 64 ? 1 : 2);  // log2(rows per 256 B)
+  static_assert((2 * NKI) % NW == 0, "loads must split evenly over waves");
+  // O is rescaled only when a row maximum grows by more than this (log2
+  // units); until then p = exp2(s - m_ref) <= 2^8.
+  constexpr float kRescale = 8.f;
 
-  __shared__ u32x4_t k_lds[2][K_CHUNKS];
-  __shared__ u32x2_t v_lds[2][NQ * D];
-  // The row's list (and soft biases) staged once: reading them from LDS in
-  // the loop keeps global loads out of the way of the K/V prefetch.
+  __shared__ __attribute__((aligned(1024))) char stage_lds[S * STAGEB];
   __shared__ int32_t list_lds[kListCache];
   __shared__ float bias_lds[kListCache];
 
@@ -236,7 +267,8 @@ void prefill_mfma_kernel(FwdParams p) {
   const int total = count * spb;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   for (int t = tid; t < count; t += NT) {
     list_lds[t] = list[t];
     if (p.sb) bias_lds[t] = load_bias(p, z, h, qb, t);
@@ -247,190 +279,241 @@ void prefill_mfma_kernel(FwdParams p) {
   const int qpos = qw0 + li;
   const int N = p.N;
 
-  const T* qp = static_cast<const T*>(p.q) + z * p.qs0 + h * p.qs1;
-  const T* kp = static_cast<const T*>(p.k) + z * p.ks0 + kvh * p.ks1;
-  const T* vp = static_cast<const T*>(p.v) + z * p.vs0 + kvh * p.vs1;
+  const char* qbase = reinterpret_cast<const char*>(static_cast<const T*>(p.q) + z * p.qs0 + h * p.qs1);
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + z * p.ks0 + kvh * p.ks1);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + z * p.vs0 + kvh * p.vs1);
+  const uint32_t qsb = static_cast<uint32_t>(p.qs2) * 2u;
+  const uint32_t ksb = static_cast<uint32_t>(p.ks2) * 2u;
+  const uint32_t vsb = static_cast<uint32_t>(p.vs2) * 2u;
 
   // Q^T operand, resident for the whole row: lane (li + 32 kh) holds
-  // Q[qpos][16 s + 8 kh .. +8].
-  // Rows past N are clamped to row N-1 (never stored): every load is
-  // unconditional, so the compiler can count outstanding loads exactly.
+  // Q[qpos][16 s + 8 kh .. +8]. Rows past N read row N-1 (never stored).
+  // A negative scale is folded into Q's sign so that c = |scale| > 0 and the
+  // row maximum of the raw dot products maps to the maximum score.
+  const uint32_t qsign = p.qk_scale < 0.f ? 0x80008000u : 0u;
+  const float c = fmaxf(fabsf(p.qk_scale), 1e-30f);
   u32x4_t qf[KS];
-  const int qrow = qpos < N ? qpos : N - 1;
+  {
+    const uint32_t qoff = __umul24(static_cast<uint32_t>(min(qpos, N - 1)), qsb) + 16u * kh;
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    qf[s] = *reinterpret_cast<const u32x4_t*>(qp + qrow * p.qs2 + 16 * s + 8 * kh);
+    for (int s = 0; s < KS; ++s) {
+      qf[s] = *reinterpret_cast<const u32x4_t*>(qbase + qoff + 32u * s) ^ qsign;
+    }
+  }
+
+  // ---- LDS layout of a stage: K tile then V tile, BN rows of ROWB bytes,
+  // 16-byte chunk c of row r stored at position c ^ f(r):
+  //   K: f = (r >> RSH) & (CPR-1)  -> the 16 rows read by one MFMA operand
+  //      fetch hit 16 distinct bank groups;
+  //   V: f = 2 (r & 3) & (CPR-1)   -> the 4 rows x 32 bytes of one transpose
+  //      read (ds_read_b64_tr_b16) hit distinct bank groups.
+  auto fk = [](int r) { return (r >> RSH) & (CPR - 1); };
+  auto fv = [](int r) { return (2 * (r & 3)) & (CPR - 1); };
+
+  // Direct-to-LDS loads: load i of this wave fills 1-KB block `blk` of the
+  // K (isk) or V tile: lane L writes slot 64 blk + L = (row, position), and
+  // fetches the global chunk that belongs at that position.
+  uint32_t goff[LPW];   // byte offset of the lane's chunk from the tile's first row
+  int grow[LPW];        // the lane's row inside the tile
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int q = wave * LPW + i;
+    const bool isk = q < NKI;
+    const int slot = (isk ? q : q - NKI) * 64 + lane;
+    const int r = slot / CPR, pos = slot % CPR;
+    const int cc = pos ^ (isk ? fk(r) : fv(r));
+    grow[i] = r;
+    goff[i] = __umul24(static_cast<uint32_t>(r), isk ? ksb : vsb) + 16u * cc;
+  }
+  // Tile m covers keys list[m / spb] * RB + (m % spb) * BN .. +BN; spb is a
+  // power of two (route_block / 32).
+  const int lspb = __builtin_ctz(spb);
+  auto tile_key0 = [&](int m) { return list_lds[m >> lspb] * p.RB + (m & (spb - 1)) * BN; };
+  const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SA_LDS char*)stage_lds));
+  auto issue = [&](int key0, int stg) {
+    const bool full = key0 >= 0 && key0 + BN <= N;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int q = wave * LPW + i;
+      const bool isk = q < NKI;
+      const char* gb = isk ? kbase : vbase;
+      const uint32_t rs = isk ? ksb : vsb;
+      const char* src;
+      if (full) {
+        src = gb + static_cast<size_t>(key0) * rs + goff[i];
+      } else {
+        // Rows outside [0, N) read a valid row: their scores are masked to
+        // -inf, so p = 0 and the data never reaches the output.
+        const uint32_t rr = static_cast<uint32_t>(min(max(key0 + grow[i], 0), N - 1));
+        src = gb + __umul24(rr, rs) + (goff[i] - __umul24(static_cast<uint32_t>(grow[i]), rs));
+      }
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(
+          lds_base + stg * STAGEB + (isk ? 0 : TILEB) + (isk ? q : q - NKI) * 1024);
+      dma16(src, dst);
+    }
+  };
+
+  // LDS read addresses (lane bases; stage / k-step / tile offsets are immediates).
+  // K operand of S^T: lane (m + 32 kh) reads row m, chunk 2 s + kh.
+  uint32_t k_rd[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) k_rd[s] = li * ROWB + 16 * ((2 * s + kh) ^ fk(li));
+  // V^T operand of O^T += V^T P^T via transpose reads: in each 16-lane group
+  // (g = lane / 16, j = lane % 16) lane j addresses row 4 kh + (j >> 2)
+  // (+ 16 s2 + 8 for the second half) and columns 4 (j & 3) + 16 (g & 1) of
+  // the 32-column tile dt; the hardware hands lane i the values of column
+  // i (+16 (g & 1)) of the four addressed rows.
+  uint32_t v_rd_even, v_rd_odd;
+  {
+    const int g = lane >> 4, j = lane & 15;
+    const int vr = 4 * kh + (j >> 2);
+    const int clane = ((j & 3) >> 1) + 2 * (g & 1);
+    const int f = fv(vr);
+    const uint32_t b = TILEB + vr * ROWB + 16 * (clane ^ (f & 3)) + 8 * (j & 1);
+    const int flip = f >> 2;   // chunk bit 2 of the swizzle flips the dt parity
+    v_rd_even = b + 64 * flip;
+    v_rd_odd = b - 64 * flip;
   }
 
   f32x16_t acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16_t{};
   float m_i = -INFINITY, l_i = 0.f;
-
-  u32x4_t kreg[KPT];
-  u32x4_t vreg[VPT][4];
-
-  auto tile_key0 = [&](int n) { return list_lds[n / spb] * p.RB + (n % spb) * BN; };
-
-  // Keys outside [0, N) load row 0 instead (branch-free, always in bounds):
-  // their scores are masked to -inf, so p = 0 exactly and the finite data
-  // they bring never reaches the output.
-  auto clamp_key = [&](int key) { return static_cast<unsigned>(key) < static_cast<unsigned>(N) ? key : 0; };
-  auto load_tile = [&](int n) {
-    const int key0 = tile_key0(n);
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int ci = tid + i * NT;
-      if (K_CHUNKS % NT == 0 || ci < K_CHUNKS) {
-        const int j = ci / CPR, c = ci % CPR;
-        kreg[i] = *reinterpret_cast<const u32x4_t*>(kp + clamp_key(key0 + j) * p.ks2 + 8 * c);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int pi = tid + i * NT;
-      if (V_PAIRS % NT == 0 || pi < V_PAIRS) {
-        const int q4 = pi / CPR, c = pi % CPR;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          vreg[i][r] = *reinterpret_cast<const u32x4_t*>(vp + clamp_key(key0 + 4 * q4 + r) * p.vs2 + 8 * c);
-        }
-      }
-    }
-  };
-
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int ci = tid + i * NT;
-      if (K_CHUNKS % NT == 0 || ci < K_CHUNKS) {
-        const int j = ci / CPR, c = ci % CPR;
-        k_lds[buf][j * CPR + (c ^ (j & (CPR - 1)))] = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int pi = tid + i * NT;
-      if (V_PAIRS % NT == 0 || pi < V_PAIRS) {
-        const int q4 = pi / CPR, c = pi % CPR;
-        // Entry for column 8c + e: the four keys' 16-bit values of that column.
-        u32x2_t ent[8];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t r0 = vreg[i][0][w], r1 = vreg[i][1][w];
-          const uint32_t r2 = vreg[i][2][w], r3 = vreg[i][3][w];
-          ent[2 * w] = u32x2_t{(r0 & 0xffffu) | (r1 << 16), (r2 & 0xffffu) | (r3 << 16)};
-          ent[2 * w + 1] = u32x2_t{(r0 >> 16) | (r1 & 0xffff0000u), (r2 >> 16) | (r3 & 0xffff0000u)};
-        }
-        u32x4_t* dst = reinterpret_cast<u32x4_t*>(&v_lds[buf][q4 * D + 8 * c]);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          dst[w] = u32x4_t{ent[2 * w][0], ent[2 * w][1], ent[2 * w + 1][0], ent[2 * w + 1][1]};
-        }
-      }
-    }
-  };
-
-  if (total > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  // Wait for every outstanding load (Q included) on all paths into the loop,
-  // so the loop's waits only ever cover its own prefetch.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
   int cur_t = -1;
   float bias = 0.f;
-  for (int n = 0; n < total; ++n) {
-    const int buf = n & 1;
-    // Everything this tile needs from memory other than LDS is read before
-    // the next tile's prefetch is issued (loads complete in order).
-    const int key0 = tile_key0(n);
-    const int t = n / spb;
+
+  auto compute = [&](int n, int key0, int stg) {
+    const int t = n >> lspb;
     if (p.sb && t != cur_t) {
       bias = bias_lds[t];
       cur_t = t;
     }
-    if (n + 1 < total) load_tile(n + 1);
+    const bool skip = qw0 >= N || static_cast<unsigned>(key0) >= static_cast<unsigned>(N) ||
+                      (CAUSAL && key0 > qw0 + 31);
+    if (skip) return;
+    char* sbase = stage_lds + stg * STAGEB;
 
-    const bool skip = qw0 >= N || static_cast<unsigned>(key0) >= static_cast<unsigned>(N) || (CAUSAL && key0 > qw0 + 31);
-    if (!skip) {
-      const bool need_mask = key0 + BN > N || (CAUSAL && key0 + BN - 1 > qw0);
+    // S^T = K Q^T (raw dot products); register v of lane (i + 32 h) holds key
+    // 8 (v >> 2) + 4 h + (v & 3) of query i.
+    u32x4_t ka[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) ka[s] = *reinterpret_cast<const u32x4_t*>(sbase + k_rd[s]);
+    // Two independent accumulation chains halve the dependent-MFMA latency.
+    f32x16_t st = f32x16_t{}, st2 = f32x16_t{};
+#pragma unroll
+    for (int s = 0; s < KS; s += 2) {
+      st = Mma<T>::mma(ka[s], qf[s], st);
+      st2 = Mma<T>::mma(ka[s + 1], qf[s + 1], st2);
+    }
+    st += st2;
 
-      f32x16_t st[ST];
+    const bool need_mask = key0 + BN > N || (CAUSAL && key0 + BN - 1 > qw0);
+    if (need_mask) {
+      int lim = N - 1 - key0;
+      if (CAUSAL) lim = min(lim, qpos - key0);
+      lim -= 4 * kh;
 #pragma unroll
-      for (int t2 = 0; t2 < ST; ++t2) {
-        st[t2] = f32x16_t{};
-        const int j = 32 * t2 + li;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const u32x4_t a = k_lds[buf][j * CPR + ((2 * s + kh) ^ (j & (CPR - 1)))];
-          st[t2] = Mma<T>::mma(a, qf[s], st[t2]);
-        }
+      for (int v = 0; v < 16; ++v) {
+        if (8 * (v >> 2) + (v & 3) > lim) st[v] = -INFINITY;
       }
-
-      float mloc = -INFINITY;
+    }
+    float mraw = st[0];
 #pragma unroll
-      for (int t2 = 0; t2 < ST; ++t2) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float sv = st[t2][v] * p.qk_scale + bias;
-          if (need_mask) {
-            const int key = key0 + 32 * t2 + 8 * (v >> 2) + 4 * kh + (v & 3);
-            if (key >= N || (CAUSAL && key > qpos)) sv = -INFINITY;
-          }
-          st[t2][v] = sv;
-          mloc = fmaxf(mloc, sv);
-        }
-      }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const float m_new = fmaxf(m_i, mloc);
-      const float m_ref = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m_i - m_ref);
+    for (int v = 1; v < 16; ++v) mraw = fmaxf(mraw, st[v]);
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mraw), __float_as_uint(mraw), false, false);
+      mraw = fmaxf(mraw, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+    }
+    const float mtile = mraw * c + bias;   // this tile's row max, scaled log2 units
+    if (__any(mtile > m_i + kRescale)) {
+      const float m_new = fmaxf(m_i, mtile);
+      const float alpha = fast_exp2(m_i - (m_new == -INFINITY ? 0.f : m_new));
       l_i *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
       m_i = m_new;
-
-      u32x4_t pb[PS];
+    }
+    const float nb = bias - (m_i == -INFINITY ? 0.f : m_i);
+    u32x4_t pb[2];
 #pragma unroll
-      for (int s2 = 0; s2 < PS; ++s2) {
-        float pv[8];
+    for (int s2 = 0; s2 < 2; ++s2) {
+      float pv[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pv[e] = fast_exp2(st[s2 >> 1][8 * (s2 & 1) + e] - m_ref);
-          l_i += pv[e];
-        }
-        pb[s2] = u32x4_t{Mma<T>::pack(pv[0], pv[1]), Mma<T>::pack(pv[2], pv[3]),
-                         Mma<T>::pack(pv[4], pv[5]), Mma<T>::pack(pv[6], pv[7])};
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = fast_exp2(fmaf(st[8 * s2 + e], c, nb));
+        l_i += pv[e];
       }
+      pb[s2] = u32x4_t{Mma<T>::pack(pv[0], pv[1]), Mma<T>::pack(pv[2], pv[3]),
+                       Mma<T>::pack(pv[4], pv[5]), Mma<T>::pack(pv[6], pv[7])};
+    }
+    // O^T += V^T P^T. MFMA k-index 8 kh + e of step s2 is key 16 s2 + 4 kh + e
+    // (e < 4) or 16 s2 + 8 + 4 kh + (e - 4): the first / second transpose read.
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint32_t vb = (dt & 1) ? v_rd_odd : v_rd_even;
 #pragma unroll
-        for (int s2 = 0; s2 < PS; ++s2) {
-          const u32x2_t lo = v_lds[buf][(4 * s2 + kh) * D + 32 * dt + li];
-          const u32x2_t hi = v_lds[buf][(4 * s2 + 2 + kh) * D + 32 * dt + li];
-          acc[dt] = Mma<T>::mma(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pb[s2], acc[dt]);
-        }
+      for (int s2 = 0; s2 < 2; ++s2) {
+        SA_LDS s16x4_t* a0 = (SA_LDS s16x4_t*)((SA_LDS char*)sbase + vb + (16 * s2) * ROWB + 64 * dt);
+        SA_LDS s16x4_t* a1 = (SA_LDS s16x4_t*)((SA_LDS char*)sbase + vb + (16 * s2 + 8) * ROWB + 64 * dt);
+        const u32x2_t lo = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(a0));
+        const u32x2_t hi = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(a1));
+        acc[dt] = Mma<T>::mma(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pb[s2], acc[dt]);
       }
     }
+  };
 
-    if (n + 1 < total) store_tile(buf ^ 1);
-    __syncthreads();
+  // No compiler-visible load may be outstanding once the pipeline runs (the
+  // explicit vmcnt waits below count only the pipeline's own loads).
+  __builtin_amdgcn_s_waitcnt(0);
+  // Pipeline: tiles n+1 .. n+S-2 stay in flight while tile n is computed;
+  // tile n+S-1 is issued into the stage tile n-1 used, once every wave has
+  // passed the barrier that follows tile n-1's compute.
+  // Key offsets of the tiles held by each stage live in registers; the list
+  // entry of the next tile to issue is read one iteration ahead.
+  int key_of[S];
+#pragma unroll
+  for (int st0 = 0; st0 < S - 1; ++st0) {
+    key_of[st0] = st0 < total ? tile_key0(st0) : 0;
+    if (st0 < total) issue(key_of[st0], st0);
+  }
+  int next_key = S - 1 < total ? tile_key0(S - 1) : 0;
+  int n = 0;
+  auto step = [&](auto stg_c) {
+    constexpr int stg = decltype(stg_c)::value;
+    if (n >= total) return;
+    const int after = total - 1 - n;   // tiles issued after tile n (capped at S - 2)
+    if (after >= 2) wait_vmcnt<2 * LPW>();
+    else if (after == 1) wait_vmcnt<LPW>();
+    else wait_vmcnt<0>();
+    barrier_only();
+    if (n + S - 1 < total) {
+      constexpr int nst = (stg + S - 1) % S;
+      key_of[nst] = next_key;
+      issue(next_key, nst);
+      if (n + S < total) next_key = tile_key0(n + S);
+    }
+    compute(n, key_of[stg], stg);
+    ++n;
+  };
+  static_assert(S == 4, "the loop below is unrolled for 4 stages");
+  while (n < total) {
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
   }
 
   const float l_tot = l_i + __shfl_xor(l_i, 32);
   if (qpos < N) {
-    const float l_safe = l_tot == 0.f ? 1.f : l_tot;
+    const float inv = 1.f / (l_tot == 0.f ? 1.f : l_tot);
     T* op = static_cast<T*>(p.out) + z * p.os0 + h * p.os1 + qpos * p.os2;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * dt + 8 * g + 4 * kh;
-        const u32x2_t val{Mma<T>::pack(acc[dt][4 * g] / l_safe, acc[dt][4 * g + 1] / l_safe),
-                          Mma<T>::pack(acc[dt][4 * g + 2] / l_safe, acc[dt][4 * g + 3] / l_safe)};
+        const u32x2_t val{Mma<T>::pack(acc[dt][4 * g] * inv, acc[dt][4 * g + 1] * inv),
+                          Mma<T>::pack(acc[dt][4 * g + 2] * inv, acc[dt][4 * g + 3] * inv)};
         *reinterpret_cast<u32x2_t*>(op + d) = val;
       }
     }
@@ -457,23 +540,23 @@ int launch_generic(FwdParams& p, int D, hipStream_t stream) {
   return check_launch("block-sparse prefill (generic) kernel");
 }
 
-template <typename T, int D, int NW, int BN>
+template <typename T, int D, int NW>
 void launch_mfma_shape(FwdParams& p, hipStream_t stream) {
   p.mtiles = (p.N + NW * 32 - 1) / (NW * 32);
   p.total_wg = p.Z * p.H * p.mtiles;
   dim3 g(p.total_wg), b(NW * 64);
   if (p.is_causal)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, BN, true>), g, b, 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, true>), g, b, 0, stream, p);
   else
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, BN, false>), g, b, 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, false>), g, b, 0, stream, p);
 }
 
 template <typename T, int D>
 int launch_mfma_d(FwdParams& p, hipStream_t stream) {
   const int RB = p.RB;
-  if (RB % 128 == 0) launch_mfma_shape<T, D, 4, 64>(p, stream);
-  else if (RB == 64) launch_mfma_shape<T, D, 2, 64>(p, stream);
-  else launch_mfma_shape<T, D, 1, 32>(p, stream);  // RB == 32
+  if (RB % 128 == 0) launch_mfma_shape<T, D, 4>(p, stream);
+  else if (RB == 64) launch_mfma_shape<T, D, 2>(p, stream);
+  else launch_mfma_shape<T, D, 1>(p, stream);  // RB == 32
   return check_launch("block-sparse prefill (MFMA) kernel");
 }
 
@@ -546,8 +629,12 @@ extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, 
                        p.qs1 % 8 == 0 && p.ks1 % 8 == 0 && p.vs1 % 8 == 0 && p.os1 % 8 == 0 &&
                        p.qs0 % 8 == 0 && p.ks0 % 8 == 0 && p.vs0 % 8 == 0 && p.os0 % 8 == 0 &&
                        aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out);
+  // 24-bit row index / row stride multiplies and 32-bit per-head byte spans.
+  const long long max_rs = std::max({p.qs2, p.ks2, p.vs2}) * 2;
+  const bool offs_ok = N < (1 << 24) && max_rs < (1 << 24) &&
+                       static_cast<long long>(N) * max_rs < (1LL << 32);
   const bool mfma_ok = dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128) &&
-                       route_block >= 32 && rows_ok && max_count <= kListCache;
+                       route_block >= 32 && rows_ok && offs_ok && max_count <= kListCache;
   const long long wg = static_cast<long long>(Z) * H * ((N + 15) / 16);
   if (wg > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
 
