@@ -199,8 +199,8 @@ def main():
         w = wl.config4(device=dev)
         kw = dict(req_depth=w.req_depth, local_blocks=w.local_blocks, sink_block=w.sink_block)
         b_alg, upages = wl.decode_routed_bytes(w)
-        ws = torch.empty(nat.lib().sa_decode_workspace_bytes(64, 32, 128, w.block_tables.shape[1]),
-                         dtype=torch.uint8, device=dev)
+        ws_bytes = nat.lib().sa_decode_workspace_bytes(64, 32, 8, 128, w.block_tables.shape[1])
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
 
         def dec():
             return ultrametric_decode(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.router,

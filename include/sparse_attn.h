@@ -131,10 +131,13 @@ int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, 
 
 /*
  * Workspace bytes needed by sa_sparse_paged_decode for B sequences of H query
- * heads of dimension D with at most max_pages logical pages each.
+ * heads (H_kv kv heads) of dimension D with at most max_pages logical pages
+ * each. 0 when B * H_kv work items already fill the GPU, so that each
+ * (sequence, kv head) is handled by one workgroup and no split-KV partials
+ * are kept; otherwise room for the per-split (max, sum, acc[D]) partials.
  * No reference counterpart (the reference decode keeps no split-KV partials).
  */
-size_t sa_decode_workspace_bytes(int B, int H, int D, int max_pages);
+size_t sa_decode_workspace_bytes(int B, int H, int H_kv, int D, int max_pages);
 
 /*
  * Sparse paged decode with tree-routed page selection.

@@ -11,18 +11,23 @@
 // h / (H / H_kv), and each K/V page is loaded once for the G = H / H_kv query
 // heads of its group.
 //
-// Kernel 1 (decode_split_kernel): one workgroup per (b, kv head, range of
-// kPagesPerSplit logical pages). Phase A: one thread per page reads the block
-// table entry and the G routing vectors, builds a G-bit head mask, and the
-// selected pages are compacted in ascending order into LDS (wave ballot +
-// per-wave prefix). Phase B: the 4 waves take selected pages round-robin;
-// within a wave, 16 lanes cover one token row of D elements with one vector
-// load each and the 4 lane groups take tokens g, g+4, ... of the page; every
-// lane group keeps its own online-softmax state per head (base-2), so no
-// cross-group traffic happens per page. Phase C: lane groups and waves are
-// merged; the (m, l, acc[D]) partial of each head is written to the
-// workspace. Kernel 2 (decode_merge_kernel) combines the partials of the
-// splits of each (b, h) and writes out.
+// decode_kernel: one workgroup (4 waves) per (sequence b, kv head, split).
+// A split owns a contiguous range of logical pages (one split unless
+// B * H_kv is too small to fill the GPU) and walks it 1024 pages at a time:
+//   phase A — every thread loads the block-table entries of 4 pages, then the
+//     G routing vectors of each (one 16-byte load per head when the router
+//     rows allow it), builds a G-bit head mask, and the selected pages are
+//     compacted into LDS in ascending logical order (wave ballot + per-wave
+//     prefix);
+//   phase B — the 4 waves take selected pages round-robin, prefetching their
+//     next page while computing the current one. 16 lanes cover one token row
+//     of D elements (one vector load each) and the 4 lane groups take tokens
+//     g, g+4, ... of the page; each lane group keeps its own base-2
+//     online-softmax state per head, so no cross-lane traffic happens per page.
+// The state survives across ranges in registers. At the end lane groups and
+// waves are merged; with one split the workgroup writes out directly,
+// otherwise it writes (m, l, acc[D]) partials that decode_merge_kernel
+// combines.
 #include "sa_internal.h"
 
 namespace sa {
@@ -30,9 +35,10 @@ namespace {
 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = kDecWaves * 64;
-constexpr int kPagesPerSplit = kDecThreads;  // phase A: one page per thread
+constexpr int kChunksPerRange = 4;                       // pages per thread per range
+constexpr int kRange = kDecThreads * kChunksPerRange;    // 1024 pages staged per pass
 constexpr int kMaxTD = 64;
-constexpr int kMaxG = 8;
+constexpr int kTargetWorkgroups = 512;                   // ~2 per CU on MI355X
 
 struct DecParams {
   const void* q;
@@ -45,6 +51,7 @@ struct DecParams {
   void* out;
   float* part;
   int B, H, Hkv, D, PS, TD, max_pages, P, r, local, sink, G, splits;
+  int vec_router;  // router rows allow one 16-byte load of 4 levels per (page, head)
   int64_t qs0, qs1, qs2;
   int64_t ks0, ks1, ks2;
   int64_t vs0, vs1, vs2;
@@ -55,38 +62,70 @@ struct DecParams {
   float qk_scale;
 };
 
-// Load DPL consecutive elements (unit stride, DPL*sizeof(T) aligned) as floats.
+// DPL consecutive elements (unit stride) kept as raw 32-bit words.
 template <typename T, int DPL>
-__device__ __forceinline__ void load_row(const T* ptr, float (&x)[DPL]) {
-  if constexpr (sizeof(T) == 2 && DPL == 8) {
-    const uint4 u = *reinterpret_cast<const uint4*>(ptr);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+struct RowRegs {
+  static constexpr int kWords = DPL * static_cast<int>(sizeof(T)) / 4 > 0 ? DPL * static_cast<int>(sizeof(T)) / 4 : 1;
+  uint32_t w[kWords];
+};
+
+template <typename T, int DPL>
+__device__ __forceinline__ void load_row(const T* ptr, RowRegs<T, DPL>& r) {
+  constexpr int BYTES = DPL * static_cast<int>(sizeof(T));
+  if constexpr (BYTES % 16 == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[2 * i] = Elem<T>::load(reinterpret_cast<const T*>(&w[i]));
-      x[2 * i + 1] = Elem<T>::load(reinterpret_cast<const T*>(&w[i]) + 1);
+    for (int i = 0; i < BYTES / 16; ++i) {
+      const uint4 u = reinterpret_cast<const uint4*>(ptr)[i];
+      r.w[4 * i] = u.x; r.w[4 * i + 1] = u.y; r.w[4 * i + 2] = u.z; r.w[4 * i + 3] = u.w;
     }
-  } else if constexpr (sizeof(T) == 2 && DPL == 4) {
+  } else if constexpr (BYTES == 8) {
     const uint2 u = *reinterpret_cast<const uint2*>(ptr);
-    const uint32_t w[2] = {u.x, u.y};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      x[2 * i] = Elem<T>::load(reinterpret_cast<const T*>(&w[i]));
-      x[2 * i + 1] = Elem<T>::load(reinterpret_cast<const T*>(&w[i]) + 1);
-    }
-  } else if constexpr (sizeof(T) == 4 && DPL % 4 == 0) {
-#pragma unroll
-    for (int i = 0; i < DPL / 4; ++i) {
-      const float4 u = *reinterpret_cast<const float4*>(ptr + 4 * i);
-      x[4 * i] = u.x;
-      x[4 * i + 1] = u.y;
-      x[4 * i + 2] = u.z;
-      x[4 * i + 3] = u.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) x[i] = Elem<T>::load(ptr + i);
+    r.w[0] = u.x; r.w[1] = u.y;
+  } else if constexpr (BYTES == 4) {
+    r.w[0] = *reinterpret_cast<const uint32_t*>(ptr);
+  } else {  // 2 bytes (one 16-bit element)
+    r.w[0] = *reinterpret_cast<const uint16_t*>(ptr);
   }
+}
+
+template <typename T, int DPL>
+__device__ __forceinline__ float row_elem(const RowRegs<T, DPL>& r, int e) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(r.w[e]);
+  } else {
+    const uint32_t word = r.w[e >> 1];
+    const uint32_t bits = (e & 1) ? (word >> 16) : (word & 0xffffu);
+    if constexpr (std::is_same<T, bf16_t>::value) return bf16_bits_to_float(bits);
+    else return f16_bits_to_float(bits);
+  }
+}
+
+// Raw bits of one element (16-bit types zero-extended).
+template <typename T>
+__device__ __forceinline__ uint32_t elem_bits(const T* p) {
+  if constexpr (sizeof(T) == 4) return __float_as_uint(*reinterpret_cast<const float*>(p));
+  else return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// Dot product of two rows held as raw words (same packing as RowRegs): packed
+// 2-element dot products with fp32 accumulation for bf16 / f16
+// (v_dot2c_f32_bf16 / v_dot2c_f32_f16; both products are exact in fp32), fp32
+// FMAs otherwise.
+template <typename T, int DPL>
+__device__ __forceinline__ float row_dot(const uint32_t* a, const RowRegs<T, DPL>& b) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < RowRegs<T, DPL>::kWords; ++i) {
+    if constexpr (std::is_same<T, bf16_t>::value) {
+      s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a[i]), __builtin_bit_cast(bf16x2_t, b.w[i]), s,
+                                          false);
+    } else if constexpr (std::is_same<T, f16_t>::value) {
+      s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a[i]), __builtin_bit_cast(f16x2_t, b.w[i]), s, false);
+    } else {
+      s = fmaf(__uint_as_float(a[i]), __uint_as_float(b.w[i]), s);
+    }
+  }
+  return s;
 }
 
 __device__ __forceinline__ uint32_t lanes_below(uint64_t ballot) {
@@ -95,113 +134,157 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t ballot) {
 }
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecParams p) {
+__global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
   constexpr int DPL = D / 16;
-  __shared__ int32_t sel_phys[kPagesPerSplit];
-  __shared__ int32_t sel_meta[kPagesPerSplit];
+  __shared__ int32_t sel_phys[kRange];
+  __shared__ int32_t sel_meta[kRange];
   __shared__ int32_t qroute[G][kMaxTD];
   __shared__ int32_t wave_count[kDecWaves];
   __shared__ float red_m[kDecWaves][G];
   __shared__ float red_l[kDecWaves][G];
   __shared__ float red_acc[kDecWaves][G][D];
 
-  const int split = blockIdx.x % p.splits;
-  const int bk = blockIdx.x / p.splits;
+  // Work items ordered (b, kv head, split); consecutive items (the kv heads of
+  // one sequence, which read the same block-table row and router rows) share
+  // an XCD.
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int split = work % p.splits;
+  const int bk = work / p.splits;
   const int kvh = bk % p.Hkv;
   const int b = bk / p.Hkv;
-  const int ctx = p.ctx[b];
-  if (ctx <= 0) return;
-  int n = (ctx + p.PS - 1) / p.PS;
-  if (n > p.max_pages) n = p.max_pages;  // block table bound (memory safety)
-  const int l0 = split * kPagesPerSplit;
-  if (l0 >= n) return;
-  const int l1 = min(n, l0 + kPagesPerSplit);
-
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h0 = kvh * G;
+  const int ctx = p.ctx[b];
+  int n = ctx > 0 ? (ctx + p.PS - 1) / p.PS : 0;
+  if (n > p.max_pages) n = p.max_pages;  // block-table bound (memory safety)
+  // This split's logical page range [pa, pz).
+  const int pa = static_cast<int>((static_cast<long long>(n) * split) / p.splits);
+  const int pz = static_cast<int>((static_cast<long long>(n) * (split + 1)) / p.splits);
 
   for (int i = tid; i < G * p.r; i += kDecThreads) {
     const int g = i / p.r, lev = i % p.r;
     qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
   }
   __syncthreads();
-
-  // ---- phase A: select and compact ------------------------------------------
-  const int l = l0 + tid;
-  int mask = 0, phys = 0;
-  if (l < l1) {
-    phys = p.bt[b * p.bts0 + l * p.bts1];
-    if (phys >= 0 && phys < p.P) {
-      const bool forced = (p.sink && l == 0) || (p.local > 0 && l >= n - p.local);
+  // First four levels of each head's query route (vector path); uniform, so
+  // they live in scalar registers.
+  int qv4[G][4];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        bool m = true;
-        if (!forced) {
-          const int32_t* rv = p.router + phys * p.rs0 + (h0 + g) * p.rs1;
-          for (int lev = 0; lev < p.r; ++lev) {
-            if (rv[lev * p.rs2] != qroute[g][lev]) {
-              m = false;
-              break;
-            }
-          }
-        }
-        if (m) mask |= 1 << g;
-      }
-    }
-  }
-  const uint64_t bal = __ballot(mask != 0);
-  if (lane == 0) wave_count[wave] = __popcll(bal);
-  __syncthreads();
-  int base = 0, nsel = 0;
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-  for (int w = 0; w < kDecWaves; ++w) {
-    if (w < wave) base += wave_count[w];
-    nsel += wave_count[w];
-  }
-  if (mask != 0) {
-    const int pos = base + static_cast<int>(lanes_below(bal));
-    sel_phys[pos] = phys;
-    sel_meta[pos] = (l - l0) | (mask << 16);
-  }
-  __syncthreads();
+    for (int lev = 0; lev < 4; ++lev) qv4[g][lev] = __builtin_amdgcn_readfirstlane(lev < p.r ? qroute[g][lev] : 0);
 
-  // ---- phase B: gather + attend ---------------------------------------------
   const int grp = lane >> 4, sub = lane & 15;
-  float qv[G][DPL];
+  constexpr int QW = RowRegs<T, DPL>::kWords;
+  uint32_t qw[G][QW];  // this lane's D/16 query elements per head, raw
   float m_s[G], l_s[G], acc[G][DPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const T* qp = static_cast<const T*>(p.q) + b * p.qs0 + (h0 + g) * p.qs1 + sub * DPL * p.qs2;
 #pragma unroll
+    for (int i = 0; i < QW; ++i) qw[g][i] = 0u;
+#pragma unroll
     for (int e = 0; e < DPL; ++e) {
-      qv[g][e] = Elem<T>::load(qp + e * p.qs2);
+      const uint32_t bits = elem_bits<T>(qp + e * p.qs2);
+      if constexpr (sizeof(T) == 4) qw[g][e] = bits;
+      else qw[g][e >> 1] |= bits << (16 * (e & 1));
       acc[g][e] = 0.f;
     }
     m_s[g] = -INFINITY;
     l_s[g] = 0.f;
   }
 
-  for (int i = wave; i < nsel; i += kDecWaves) {
-    const int ph = sel_phys[i];
-    const int meta = sel_meta[i];
-    const int lp = l0 + (meta & 0xffff);
-    const int hmask = meta >> 16;
-    const int valid = min(p.PS, ctx - lp * p.PS);
-    const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvh * p.ks1 + sub * DPL;
-    const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvh * p.vs1 + sub * DPL;
-    for (int tc = 0; tc < p.PS; tc += 16) {
-      float kx[4][DPL], vx[4][DPL];
+  for (int r0 = pa; r0 < pz; r0 += kRange) {
+    const int r1 = min(pz, r0 + kRange);
+    // ---- phase A: block table, routing vectors, compaction --------------------
+    int phys[kChunksPerRange];
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int tok = tc + 4 * it + grp;
-        if (tok < valid) {
-          load_row<T, DPL>(kpage + tok * p.ks2, kx[it]);
-          load_row<T, DPL>(vpage + tok * p.vs2, vx[it]);
+    for (int c = 0; c < kChunksPerRange; ++c) {
+      const int l = r0 + c * kDecThreads + tid;
+      phys[c] = l < r1 ? p.bt[b * p.bts0 + l * p.bts1] : -1;
+    }
+    int mask[kChunksPerRange];
+#pragma unroll
+    for (int c = 0; c < kChunksPerRange; ++c) {
+      const int l = r0 + c * kDecThreads + tid;
+      int m = 0;
+      if (l < r1 && phys[c] >= 0 && phys[c] < p.P) {
+        const bool forced = (p.sink && l == 0) || (p.local > 0 && l >= n - p.local);
+        if (forced) {
+          m = (1 << G) - 1;
+        } else if (p.vec_router) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const int4 rv = *reinterpret_cast<const int4*>(p.router + phys[c] * p.rs0 + (h0 + g) * p.rs1);
+            bool ok = true;
+            if (p.r > 0) ok = ok && rv.x == qv4[g][0];
+            if (p.r > 1) ok = ok && rv.y == qv4[g][1];
+            if (p.r > 2) ok = ok && rv.z == qv4[g][2];
+            if (p.r > 3) ok = ok && rv.w == qv4[g][3];
+            if (ok) m |= 1 << g;
+          }
         } else {
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) kx[it][e] = vx[it][e] = 0.f;
+          for (int g = 0; g < G; ++g) {
+            const int32_t* rv = p.router + phys[c] * p.rs0 + (h0 + g) * p.rs1;
+            bool ok = true;
+            for (int lev = 0; lev < p.r; ++lev) {
+              if (rv[lev * p.rs2] != qroute[g][lev]) {
+                ok = false;
+                break;
+              }
+            }
+            if (ok) m |= 1 << g;
+          }
         }
       }
+      mask[c] = m;
+    }
+    int nsel = 0;
+#pragma unroll
+    for (int c = 0; c < kChunksPerRange; ++c) {
+      const int l = r0 + c * kDecThreads + tid;
+      const uint64_t bal = __ballot(mask[c] != 0);
+      if (lane == 0) wave_count[wave] = __popcll(bal);
+      __syncthreads();
+      int base = nsel, tot = 0;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const int cw = wave_count[w];
+        if (w < wave) base += cw;
+        tot += cw;
+      }
+      if (mask[c] != 0) {
+        const int pos = base + static_cast<int>(lanes_below(bal));
+        sel_phys[pos] = phys[c];
+        sel_meta[pos] = (l - r0) | (mask[c] << 16);
+      }
+      nsel += tot;
+      __syncthreads();
+    }
+
+    // ---- phase B: gather + attend the selected pages ----------------------------
+    // fetch() loads K and V rows of one page into a register buffer; attend()
+    // folds a fetched page into the online softmax. Buffers are only ever
+    // indexed by compile-time constants (so they stay in registers).
+    using Rows = RowRegs<T, DPL>[4];
+    auto fetch = [&](int i, int tc, Rows& kx, Rows& vx) {
+      const int ph = sel_phys[i];
+      const int lp = r0 + (sel_meta[i] & 0xffff);
+      const int valid = min(p.PS, ctx - lp * p.PS);
+      const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvh * p.ks1 + sub * DPL;
+      const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvh * p.vs1 + sub * DPL;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int tok = min(tc + 4 * it + grp, valid - 1);   // masked rows reread a valid row
+        load_row<T, DPL>(kpage + tok * p.ks2, kx[it]);
+        load_row<T, DPL>(vpage + tok * p.vs2, vx[it]);
+      }
+    };
+    auto attend = [&](int i, int tc, const Rows& kx, const Rows& vx) {
+      const int lp = r0 + (sel_meta[i] & 0xffff);
+      const int hmask = sel_meta[i] >> 16;
+      const int valid = min(p.PS, ctx - lp * p.PS);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         if (!((hmask >> g) & 1)) continue;
@@ -209,10 +292,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecParams p) 
         float mloc = -INFINITY;
 #pragma unroll
         for (int it = 0; it < 4; ++it) {
-          float part = 0.f;
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) part = fmaf(qv[g][e], kx[it][e], part);
-          const float sc = row16_sum(part) * p.qk_scale;
+          const float sc = row16_sum(row_dot<T, DPL>(qw[g], kx[it])) * p.qk_scale;
           s[it] = (tc + 4 * it + grp) < valid ? sc : -INFINITY;
           mloc = fmaxf(mloc, s[it]);
         }
@@ -227,15 +307,53 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecParams p) 
           const float pv = fast_exp2(s[it] - m_ref);
           lsum += pv;
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(pv, vx[it][e], acc[g][e]);
+          for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(pv, row_elem<T, DPL>(vx[it], e), acc[g][e]);
         }
         l_s[g] = lsum;
         m_s[g] = m_new;
       }
+    };
+    if (p.PS <= 16) {
+      // Whole page per fetch. A wave keeps kDecBufs pages in flight: page
+      // i + (kDecBufs-1)*waves is requested before page i is folded in.
+      // Fetch indices past the end are clamped to the wave's last page (a
+      // reread that hits cache), so every iteration issues the same loads and
+      // the load counter waits stay static.
+      // Pages in flight per wave: 3 when a page costs <= 32 registers per
+      // lane (16-bit D <= 128, fp32 D <= 64), fewer for wider rows.
+      constexpr int kDecBufs = 8 * QW <= 32 ? 3 : (8 * QW <= 64 ? 2 : 1);
+      if (wave < nsel) {
+        const int last = wave + ((nsel - 1 - wave) / kDecWaves) * kDecWaves;
+        Rows kx[kDecBufs], vx[kDecBufs];
+#pragma unroll
+        for (int b2 = 0; b2 < kDecBufs - 1; ++b2) fetch(min(wave + b2 * kDecWaves, last), 0, kx[b2], vx[b2]);
+        for (int base = wave; base <= last; base += kDecBufs * kDecWaves) {
+#pragma unroll
+          for (int b2 = 0; b2 < kDecBufs; ++b2) {
+            const int i = base + b2 * kDecWaves;
+            if (i > last) break;
+            fetch(min(i + (kDecBufs - 1) * kDecWaves, last), 0, kx[(b2 + kDecBufs - 1) % kDecBufs],
+                  vx[(b2 + kDecBufs - 1) % kDecBufs]);
+            attend(i, 0, kx[b2], vx[b2]);
+          }
+        }
+      }
+    } else {
+      // Larger pages: 16 tokens at a time, no cross-page prefetch.
+      for (int i = wave; i < nsel; i += kDecWaves) {
+        const int lp = r0 + (sel_meta[i] & 0xffff);
+        const int valid = min(p.PS, ctx - lp * p.PS);
+        for (int tc = 0; tc < valid; tc += 16) {
+          Rows kx, vx;
+          fetch(i, tc, kx, vx);
+          attend(i, tc, kx, vx);
+        }
+      }
     }
+    __syncthreads();  // sel_* is rewritten by the next range
   }
 
-  // ---- phase C: merge lane groups, then waves ----------------------------------
+  // ---- merge lane groups, then waves ---------------------------------------------
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float mw = fmaxf(m_s[g], __shfl_xor(m_s[g], 16));
@@ -275,45 +393,46 @@ __global__ __launch_bounds__(kDecThreads) void decode_split_kernel(DecParams p) 
       a += red_acc[w][g][d] * sc;
       lsum += red_l[w][g] * sc;
     }
-    float* dst = p.part + ((static_cast<int64_t>(b) * p.H + h0 + g) * p.splits + split) * (D + 2);
-    dst[2 + d] = a;
-    if (d == 0) {
-      dst[0] = mx;
-      dst[1] = lsum;
+    if (p.splits == 1) {
+      T* op = static_cast<T*>(p.out) + b * p.os0 + (h0 + g) * p.os1;
+      Elem<T>::store(op + d * p.os2, lsum > 0.f ? a / lsum : 0.f);
+    } else {
+      float* dst = p.part + ((static_cast<int64_t>(b) * p.H + h0 + g) * p.splits + split) * (D + 2);
+      dst[2 + d] = a;
+      if (d == 0) {
+        dst[0] = mx;
+        dst[1] = lsum;
+      }
     }
   }
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecParams p) {
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecParams p) {
   const int bh = blockIdx.x;
   const int b = bh / p.H, h = bh % p.H;
   const int D = p.D;
   T* op = static_cast<T*>(p.out) + b * p.os0 + h * p.os1;
-  const int ctx = p.ctx[b];
-  int n = ctx > 0 ? (ctx + p.PS - 1) / p.PS : 0;
-  if (n > p.max_pages) n = p.max_pages;
-  const int nsplit = (n + kPagesPerSplit - 1) / kPagesPerSplit;
   const float* src = p.part + static_cast<int64_t>(bh) * p.splits * (D + 2);
   float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, src[s * (D + 2)]);
+  for (int s = 0; s < p.splits; ++s) mx = fmaxf(mx, src[s * (D + 2)]);
   const float mref = mx == -INFINITY ? 0.f : mx;
   float lsum = 0.f;
-  for (int s = 0; s < nsplit; ++s) lsum += src[s * (D + 2) + 1] * fast_exp2(src[s * (D + 2)] - mref);
+  for (int s = 0; s < p.splits; ++s) lsum += src[s * (D + 2) + 1] * fast_exp2(src[s * (D + 2)] - mref);
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float a = 0.f;
-    for (int s = 0; s < nsplit; ++s) a += src[s * (D + 2) + 2 + d] * fast_exp2(src[s * (D + 2)] - mref);
+    for (int s = 0; s < p.splits; ++s) a += src[s * (D + 2) + 2 + d] * fast_exp2(src[s * (D + 2)] - mref);
     Elem<T>::store(op + d * p.os2, lsum > 0.f ? a / lsum : 0.f);
   }
 }
 
 template <typename T, int D>
-void launch_split_d(DecParams& p, dim3 g, hipStream_t s) {
+void launch_d(DecParams& p, dim3 g, hipStream_t s) {
   switch (p.G) {
-    case 1: hipLaunchKernelGGL((decode_split_kernel<T, D, 1>), g, dim3(kDecThreads), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((decode_split_kernel<T, D, 2>), g, dim3(kDecThreads), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((decode_split_kernel<T, D, 4>), g, dim3(kDecThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((decode_split_kernel<T, D, 8>), g, dim3(kDecThreads), 0, s, p); break;
+    case 1: hipLaunchKernelGGL((decode_kernel<T, D, 1>), g, dim3(kDecThreads), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<T, D, 2>), g, dim3(kDecThreads), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<T, D, 4>), g, dim3(kDecThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((decode_kernel<T, D, 8>), g, dim3(kDecThreads), 0, s, p); break;
   }
 }
 
@@ -322,29 +441,38 @@ int launch_decode(DecParams& p, hipStream_t s) {
   const long long wg = static_cast<long long>(p.B) * p.Hkv * p.splits;
   if (wg > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
   dim3 g(static_cast<unsigned>(wg));
-  if (wg > 0) {
-    switch (p.D) {
-      case 16: launch_split_d<T, 16>(p, g, s); break;
-      case 32: launch_split_d<T, 32>(p, g, s); break;
-      case 64: launch_split_d<T, 64>(p, g, s); break;
-      case 128: launch_split_d<T, 128>(p, g, s); break;
-      default: launch_split_d<T, 256>(p, g, s); break;
-    }
-    int rc = check_launch("sparse paged decode kernel");
-    if (rc != SA_OK) return rc;
+  switch (p.D) {
+    case 16: launch_d<T, 16>(p, g, s); break;
+    case 32: launch_d<T, 32>(p, g, s); break;
+    case 64: launch_d<T, 64>(p, g, s); break;
+    case 128: launch_d<T, 128>(p, g, s); break;
+    default: launch_d<T, 256>(p, g, s); break;
   }
+  int rc = check_launch("sparse paged decode kernel");
+  if (rc != SA_OK || p.splits == 1) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(p.B * p.H), dim3(64), 0, s, p);
   return check_launch("sparse paged decode merge kernel");
 }
 
-int splits_for(int max_pages) { return max_pages <= 0 ? 1 : (max_pages + kPagesPerSplit - 1) / kPagesPerSplit; }
+// Splits per (sequence, kv head): enough workgroups to fill the GPU, never
+// more than one per 256 pages.
+int splits_for(int B, int H_kv, int max_pages) {
+  const long long pairs = static_cast<long long>(B) * H_kv;
+  if (pairs <= 0) return 1;
+  long long s = (kTargetWorkgroups + pairs - 1) / pairs;
+  const long long cap = max_pages <= 0 ? 1 : (max_pages + 255) / 256;
+  if (s > cap) s = cap;
+  return static_cast<int>(s < 1 ? 1 : s);
+}
 
 }  // namespace
 }  // namespace sa
 
-extern "C" size_t sa_decode_workspace_bytes(int B, int H, int D, int max_pages) {
-  if (B <= 0 || H <= 0 || D <= 0) return 0;
-  return static_cast<size_t>(B) * H * sa::splits_for(max_pages) * (D + 2) * sizeof(float);
+extern "C" size_t sa_decode_workspace_bytes(int B, int H, int H_kv, int D, int max_pages) {
+  if (B <= 0 || H <= 0 || H_kv <= 0 || D <= 0) return 0;
+  const int splits = sa::splits_for(B, H_kv, max_pages);
+  if (splits == 1) return 0;
+  return static_cast<size_t>(B) * H * splits * (D + 2) * sizeof(float);
 }
 
 extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const void* v_cache,
@@ -384,8 +512,8 @@ extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const 
   if (k_strides[3] != 1 || v_strides[3] != 1) {
     return fail(SA_EUNSUPPORTED, "k_cache / v_cache need unit stride along head_dim");
   }
-  // Each lane loads D/16 consecutive elements with one vector load (at most
-  // 16 bytes), so rows and base pointers must be aligned to that size.
+  // Each lane loads D/16 consecutive elements with vector loads of up to 16
+  // bytes, so rows and base pointers must be aligned to that size.
   const int64_t esize = dtype == SA_DTYPE_F32 ? 4 : 2;
   int64_t align = (D / 16) * esize;
   if (align > 16) align = 16;
@@ -398,8 +526,8 @@ extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const 
       reinterpret_cast<uintptr_t>(v_cache) % align != 0) {
     return fail(SA_EUNSUPPORTED, "k_cache / v_cache base pointers break vector alignment");
   }
-  const size_t need = sa_decode_workspace_bytes(B, H, D, max_pages);
-  if (!workspace || workspace_bytes < need) {
+  const size_t need = sa_decode_workspace_bytes(B, H, H_kv, D, max_pages);
+  if (need > 0 && (!workspace || workspace_bytes < need)) {
     return fail(SA_EINVAL, "workspace too small: need " + std::to_string(need) + " bytes");
   }
 
@@ -410,7 +538,9 @@ extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const 
   p.max_pages = max_pages; p.P = num_phys_pages;
   p.r = req_depth < 0 ? 0 : (req_depth > TD ? TD : req_depth);
   p.local = local_blocks; p.sink = sink_block != 0; p.G = G;
-  p.splits = splits_for(max_pages);
+  p.splits = splits_for(B, H_kv, max_pages);
+  p.vec_router = r_strides[2] == 1 && TD >= 4 && p.r <= 4 && r_strides[0] % 4 == 0 &&
+                 r_strides[1] % 4 == 0 && (reinterpret_cast<uintptr_t>(router) & 15) == 0;
   p.qs0 = q_strides[0]; p.qs1 = q_strides[1]; p.qs2 = q_strides[2];
   p.ks0 = k_strides[0]; p.ks1 = k_strides[1]; p.ks2 = k_strides[2];
   p.vs0 = v_strides[0]; p.vs1 = v_strides[1]; p.vs2 = v_strides[2];

@@ -80,14 +80,6 @@ template <> __device__ __forceinline__ float round_to<f16_t>(float x) {
 
 constexpr int kListCache = 1024;  // MFMA path: a row's list (<= 1024 blocks) lives in LDS
 
-// XCD-aware work index: workgroup b runs on XCD b % 8; give each XCD a
-// contiguous range of the T work items.
-__device__ __forceinline__ int xcd_remap(int b, int T) {
-  const int xcd = b & 7, slot = b >> 3;
-  const int q8 = T >> 3, r8 = T & 7;
-  return xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot;
-}
-
 // ============================================================================
 // Generic kernel: 16 query rows per workgroup, 16 lanes per row.
 // ============================================================================

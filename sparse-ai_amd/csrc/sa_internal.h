@@ -93,6 +93,15 @@ __device__ __forceinline__ float row16_max(float x) {
   return x;
 }
 
+// XCD-aware work index: the dispatcher places workgroup b on XCD b % 8 (MI355X
+// has 8 XCDs, each with its own L2); give each XCD a contiguous range of the T
+// work items so that neighbouring items share an L2.
+__device__ __forceinline__ int xcd_remap(int b, int T) {
+  const int xcd = b & 7, slot = b >> 3;
+  const int q8 = T >> 3, r8 = T & 7;
+  return xcd < r8 ? xcd * (q8 + 1) + slot : r8 * (q8 + 1) + (xcd - r8) * q8 + slot;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

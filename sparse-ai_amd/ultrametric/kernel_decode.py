@@ -24,9 +24,13 @@ HAS_TRITON = nat.available()
 __all__ = ["HAS_TRITON", "ultrametric_decode", "_ultrametric_decode_reference", "decode_workspace_bytes"]
 
 
-def decode_workspace_bytes(batch_size: int, num_heads: int, head_dim: int, max_pages: int) -> int:
-    """Bytes of split-KV scratch the decode kernels need."""
-    return int(nat.lib().sa_decode_workspace_bytes(batch_size, num_heads, head_dim, max_pages))
+def decode_workspace_bytes(batch_size: int, num_heads: int, head_dim: int, max_pages: int,
+                           num_kv_heads: int = None) -> int:
+    """Bytes of split-KV scratch the decode kernels need (0: none).
+
+    ``num_kv_heads`` defaults to ``num_heads`` (no GQA)."""
+    hkv = num_heads if num_kv_heads is None else num_kv_heads
+    return int(nat.lib().sa_decode_workspace_bytes(batch_size, num_heads, hkv, head_dim, max_pages))
 
 
 def ultrametric_decode(
@@ -73,9 +77,11 @@ def ultrametric_decode(
     num_pages, H_kv, page_size, _ = k_cache.shape
     max_pages = bt.shape[1]
     out = torch.empty((batch_size, num_heads, head_dim), dtype=q.dtype, device=dev)
-    need = decode_workspace_bytes(batch_size, num_heads, head_dim, max_pages)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    need = decode_workspace_bytes(batch_size, num_heads, head_dim, max_pages, H_kv)
+    if need == 0:
+        workspace = None
+    elif workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     dt = nat.dtype_code(q.dtype, (torch.float32, torch.bfloat16, torch.float16))
     lib = nat.lib()
     with torch.cuda.device(dev):
@@ -84,8 +90,9 @@ def ultrametric_decode(
             nat.ptr(qrt), nat.ptr(out), batch_size, num_heads, H_kv, head_dim, page_size, tree_depth,
             max_pages, num_pages, int(req_depth), int(local_blocks), int(bool(sink_block)),
             nat.strides(q), nat.strides(k_cache), nat.strides(v_cache), nat.strides(bt),
-            nat.strides(rt), nat.strides(qrt), nat.strides(out), nat.ptr(workspace),
-            workspace.numel(), dt, nat.stream(dev))
+            nat.strides(rt), nat.strides(qrt), nat.strides(out),
+            None if workspace is None else nat.ptr(workspace), 0 if workspace is None else workspace.numel(),
+            dt, nat.stream(dev))
     nat.check(rc)
     return out
 

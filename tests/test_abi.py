@@ -63,9 +63,12 @@ def test_host_side_argument_errors():
     args = [p] * 8 + [1, 6, 2, 64, 16, 4, 4, 10, 4, 0, 0, st3, stk, stk, st2, st3, st3, st3, p, 0, 1, None]
     assert lib.sa_sparse_paged_decode(*args) == nat.SA_EUNSUPPORTED
     args[9] = 8
+    args[14] = 300  # 300 pages for 2 (sequence, kv head) pairs: split-KV, needs a workspace
     assert lib.sa_sparse_paged_decode(*args) == nat.SA_EINVAL
     assert b"workspace" in lib.sa_last_error()
-    assert lib.sa_decode_workspace_bytes(2, 8, 64, 300) == 2 * 8 * 2 * 66 * 4
+    assert lib.sa_decode_workspace_bytes(2, 8, 8, 64, 300) == 2 * 8 * 2 * 66 * 4
+    # enough (sequence, kv head) pairs to fill the GPU: one workgroup each, no workspace
+    assert lib.sa_decode_workspace_bytes(64, 32, 8, 128, 2048) == 0
 
 
 def test_python_layer_raises_on_cpu_tensors():
