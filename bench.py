@@ -33,6 +33,20 @@ for _p in (ROOT, os.path.join(ROOT, "sparse-ai_amd")):
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def profiled_traffic(name):
+    """HBM bytes per launch recorded in profiles/<name> (rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes scaled by a 256 MiB copy; the file gives the commands), or None."""
+    path = os.path.join(PROFILES, name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        for line in fh:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    return None
 
 
 def parse_args():
@@ -42,10 +56,23 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
-    ap.add_argument("--cpu-heads", type=int, default=4, help="heads timed for the CPU baseline")
+    ap.add_argument("--cpu-heads", type=int, default=32, help="heads timed for the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="minimum CPU work for the CPU baseline (whole passes over --cpu-heads)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (reference for HBM byte counters)")
     return ap.parse_args()
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def log(msg):
@@ -175,9 +202,11 @@ def main():
         "prefill_kernel_ms": round(fwd_ms, 5),
         "build_ms": round(build_ms, 5),
         "roofline": {
-            "kernel": "prefill_mfma_kernel<bf16,128,4,64,causal>",
+            "kernel": "prefill_mfma_kernel<bf16, D=128, 4 waves, causal>",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": profiled_traffic("prefill_mfma_config2_bf16.md"),
+            "traffic_source": "profiles/prefill_mfma_config2_bf16.md",
             "unique_hbm_bytes": 4 * q.numel() * q.element_size(),
         },
     }
@@ -199,17 +228,35 @@ def main():
         w = wl.config4(device=dev)
         kw = dict(req_depth=w.req_depth, local_blocks=w.local_blocks, sink_block=w.sink_block)
         b_alg, upages = wl.decode_routed_bytes(w)
-        ws_bytes = nat.lib().sa_decode_workspace_bytes(64, 32, 8, 128, w.block_tables.shape[1])
+        B, Hq, Dd = w.q.shape
+        P, Hkv, PS, _ = w.k_cache.shape
+        TD = w.q_router.shape[-1]
+        max_pages = w.block_tables.shape[1]
+        ws_bytes = nat.lib().sa_decode_workspace_bytes(B, Hq, Hkv, Dd, max_pages)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        dout = torch.empty_like(w.q)
+        bt = w.block_tables.to(torch.int32)
+        ctxl = w.context_lens.to(torch.int32).contiguous()
+        # raw ABI launches with prebuilt arguments: the kernel, not Python call overhead
+        dargs = (nat.ptr(w.q), nat.ptr(w.k_cache), nat.ptr(w.v_cache), nat.ptr(bt), nat.ptr(ctxl),
+                 nat.ptr(w.router), nat.ptr(w.q_router), nat.ptr(dout), B, Hq, Hkv, Dd, PS, TD, max_pages, P,
+                 w.req_depth, w.local_blocks, int(w.sink_block), nat.strides(w.q), nat.strides(w.k_cache),
+                 nat.strides(w.v_cache), nat.strides(bt), nat.strides(w.router), nat.strides(w.q_router),
+                 nat.strides(dout), None if ws is None else nat.ptr(ws), ws_bytes,
+                 nat.dtype_code(w.q.dtype, (torch.float32, torch.bfloat16, torch.float16)),
+                 stream)
+        dec_fn = nat.lib().sa_sparse_paged_decode
 
         def dec():
-            return ultrametric_decode(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.router,
-                                      w.q_router, workspace=ws, **kw)
+            nat.check(dec_fn(*dargs))
 
         with torch.no_grad():
             for _ in range(args.warmup):
                 dec()
             dec_ms = time_launches(dec, max(50, args.steps), torch)
+            api_out = ultrametric_decode(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.router,
+                                         w.q_router, **kw)
+            assert torch.equal(api_out, dout), "raw-ABI decode disagrees with the public API"
         meta_bytes = int(w.context_lens.add(15).div(16, rounding_mode="floor").sum()) * (4 + 32 * 4 * 4)
         dec_gbs = b_alg / (dec_ms * 1e-3) / 1e9
         result["decode"] = {
@@ -219,8 +266,10 @@ def main():
             "routed_kv_bytes": b_alg, "unique_pages": upages,
             "routing_metadata_bytes": meta_bytes,
             "gbs_routed": round(dec_gbs, 1),
-            "roofline": {"bound": "hbm", "achieved": round(dec_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(dec_gbs / PEAK_HBM_GBS, 4), "traffic": None},
+            "roofline": {"kernel": "decode_kernel<bf16, D=128, G=4>", "bound": "hbm", "achieved": round(dec_gbs, 1),
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(dec_gbs / PEAK_HBM_GBS, 4),
+                         "traffic": profiled_traffic("decode_config4_bf16.md"),
+                         "traffic_source": "profiles/decode_config4_bf16.md"},
         }
         log(f"decode {dec_ms * 1e3:.1f} us/call, {dec_gbs:.0f} GB/s on routed bytes")
         del w
@@ -232,20 +281,27 @@ def main():
         qc, kc, vc = (t[0, heads].cpu() for t in (q, k, v))
         mk = mask[0, heads].cpu()
         oa.masked_attention_torch_fp32(qc[:1, :256], kc[:1, :256], vc[:1, :256], mk[:1, :2, :2], RB, True)
-        t0 = time.perf_counter()
-        oa.masked_attention_torch_fp32(qc, kc, vc, mk, RB, True)
-        cpu_s = time.perf_counter() - t0
+        # whole passes over the sampled heads until at least --cpu-seconds of CPU work
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            oa.masked_attention_torch_fp32(qc, kc, vc, mk, RB, True)
+            passes += 1
+            if time.perf_counter() - t0 >= args.cpu_seconds:
+                break
+        cpu_s = (time.perf_counter() - t0) / passes
         flop_sample = wl.prefill_flops(counts[0, heads], D, RB)
         result["cpu_baseline"] = {
             "value": round(flop_sample / cpu_s / 1e12, 4), "unit": "TFLOP/s",
             "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"fp32 masked-dense oracle (oracle/attention.py masked_attention_torch_fp32) on "
-                      f"{len(heads)} of {H} heads of config 2, query-chunked 2048; {cpu_s:.2f} s; "
-                      f"FLOP_alg of those heads' listed tiles / wall time",
-            "cpu_model": platform.processor() or platform.machine(),
+            "sample": f"fp32 masked-dense oracle (oracle/attention.py masked_attention_torch_fp32, the "
+                      f"reference's masked_reference_attention formulation, query-chunked 2048) on "
+                      f"{len(heads)} of {H} heads of config 2; {passes} passes, {cpu_s:.2f} s per pass; "
+                      f"value = FLOP_alg of those heads' listed tiles / wall time per pass",
+            "cpu_model": cpu_model(),
             "os_cpu_count": os.cpu_count(),
+            "torch": torch.__version__,
         }
-        log(f"cpu baseline {cpu_s:.2f} s for {len(heads)} heads")
+        log(f"cpu baseline {cpu_s:.2f} s per pass over {len(heads)} heads ({passes} passes)")
 
     print(json.dumps(result), flush=True)
 

@@ -14,7 +14,6 @@ Modules:
   attention  — token masks and masked-dense attention (out and LSE), float64
                numpy, plus the fp32 torch variant timed as the CPU baseline.
   decode     — sparse paged decode reference (GQA by head grouping).
-  surgery    — LLaMA-surgery route-block majority vote and budget statistics.
 
 Parity pinning: see the header of each module for the checks that pin it
 (known-answer tests from the reference's own tests, closed forms, brute

@@ -13,21 +13,27 @@
 //
 // decode_kernel: one workgroup (4 waves) per (sequence b, kv head, split).
 // A split owns a contiguous range of logical pages (one split unless
-// B * H_kv is too small to fill the GPU) and walks it 1024 pages at a time:
-//   phase A — every thread loads the block-table entries of 4 pages, then the
-//     G routing vectors of each (one 16-byte load per head when the router
-//     rows allow it), builds a G-bit head mask, and the selected pages are
-//     compacted into LDS in ascending logical order (wave ballot + per-wave
-//     prefix);
-//   phase B — the 4 waves take selected pages round-robin, prefetching their
-//     next page while computing the current one. 16 lanes cover one token row
-//     of D elements (one vector load each) and the 4 lane groups take tokens
-//     g, g+4, ... of the page; each lane group keeps its own base-2
-//     online-softmax state per head, so no cross-lane traffic happens per page.
+// B * H_kv is too small to fill the GPU) and walks it 4096/G pages at a time:
+//   phase A1 — G consecutive lanes share a page: all lanes load the page's
+//     block-table entry, then lane j loads head j's routing vector (one
+//     16-byte load when the router rows allow it, so a page's G vectors are
+//     one contiguous read); a ballot turns the G match bits into the page's
+//     head mask (forced pages: all heads). All 16 passes of a range issue
+//     their loads back to back;
+//   phase A2 — the selected pages are compacted into LDS in ascending logical
+//     order (per-thread counts, wave prefix sum, per-wave offsets);
+//   phase B — the 4 waves take selected pages round-robin with up to 3 pages
+//     in flight per wave (register ring indexed by compile-time constants).
+//     16 lanes cover one token row of D elements (one vector load each) and
+//     the 4 lane groups take tokens g, g+4, ... of the page; QK uses packed
+//     bf16/f16 dot products on the raw words; each lane group keeps its own
+//     base-2 online-softmax state per head, so no cross-lane traffic happens
+//     per page.
 // The state survives across ranges in registers. At the end lane groups and
 // waves are merged; with one split the workgroup writes out directly,
 // otherwise it writes (m, l, acc[D]) partials that decode_merge_kernel
-// combines.
+// combines. Consecutive work items (the kv heads of one sequence, which read
+// the same block-table and router rows) are placed on one XCD.
 #include "sa_internal.h"
 
 namespace sa {
@@ -35,8 +41,6 @@ namespace {
 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = kDecWaves * 64;
-constexpr int kChunksPerRange = 4;                       // pages per thread per range
-constexpr int kRange = kDecThreads * kChunksPerRange;    // 1024 pages staged per pass
 constexpr int kMaxTD = 64;
 constexpr int kTargetWorkgroups = 512;                   // ~2 per CU on MI355X
 
@@ -136,6 +140,15 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t ballot) {
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
   constexpr int DPL = D / 16;
+  // Phase A layout: G consecutive lanes share one page (lane j reads head j's
+  // routing vector, so a page's G vectors are one contiguous 16*G-byte read);
+  // a pass covers kPagesPerPass pages and a range kPasses passes.
+  constexpr int kPagesPerPass = kDecThreads / G;
+  constexpr int kPasses = 16;
+  constexpr int kRange = kPagesPerPass * kPasses;    // 4096 / G pages
+  constexpr int kPagesPerThread = kRange / kDecThreads;
+  __shared__ int32_t page_phys[kRange];
+  __shared__ uint8_t page_mask[kRange];
   __shared__ int32_t sel_phys[kRange];
   __shared__ int32_t sel_meta[kRange];
   __shared__ int32_t qroute[G][kMaxTD];
@@ -166,13 +179,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
     qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
   }
   __syncthreads();
-  // First four levels of each head's query route (vector path); uniform, so
-  // they live in scalar registers.
-  int qv4[G][4];
+  const int gl = tid % G;       // head (within the group) whose routing vector this lane checks
+  const int pslot = tid / G;    // page slot within a pass
+  int qmine[4];                 // this lane's head's first four query levels (vector path)
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int lev = 0; lev < 4; ++lev) qv4[g][lev] = __builtin_amdgcn_readfirstlane(lev < p.r ? qroute[g][lev] : 0);
+  for (int lev = 0; lev < 4; ++lev) qmine[lev] = lev < p.r ? qroute[gl][lev] : 0;
 
   const int grp = lane >> 4, sub = lane & 15;
   constexpr int QW = RowRegs<T, DPL>::kWords;
@@ -196,72 +207,95 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
 
   for (int r0 = pa; r0 < pz; r0 += kRange) {
     const int r1 = min(pz, r0 + kRange);
-    // ---- phase A: block table, routing vectors, compaction --------------------
-    int phys[kChunksPerRange];
+    // ---- phase A1: block table + routing vectors -> per-page head mask ---------
+    // All loads are unconditional (indices clamped into range) so they issue
+    // back to back; out-of-range results are discarded afterwards.
+    int phys[kPasses];
 #pragma unroll
-    for (int c = 0; c < kChunksPerRange; ++c) {
-      const int l = r0 + c * kDecThreads + tid;
-      phys[c] = l < r1 ? p.bt[b * p.bts0 + l * p.bts1] : -1;
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int l = min(r0 + ps * kPagesPerPass + pslot, r1 - 1);
+      phys[ps] = p.bt[b * p.bts0 + l * p.bts1];
     }
-    int mask[kChunksPerRange];
+    bool hit[kPasses];
+    if (p.vec_router) {
+      int4 rv[kPasses];
 #pragma unroll
-    for (int c = 0; c < kChunksPerRange; ++c) {
-      const int l = r0 + c * kDecThreads + tid;
-      int m = 0;
-      if (l < r1 && phys[c] >= 0 && phys[c] < p.P) {
-        const bool forced = (p.sink && l == 0) || (p.local > 0 && l >= n - p.local);
-        if (forced) {
-          m = (1 << G) - 1;
-        } else if (p.vec_router) {
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
+        rv[ps] = *reinterpret_cast<const int4*>(p.router + ph * p.rs0 + (h0 + gl) * p.rs1);
+      }
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const int4 rv = *reinterpret_cast<const int4*>(p.router + phys[c] * p.rs0 + (h0 + g) * p.rs1);
-            bool ok = true;
-            if (p.r > 0) ok = ok && rv.x == qv4[g][0];
-            if (p.r > 1) ok = ok && rv.y == qv4[g][1];
-            if (p.r > 2) ok = ok && rv.z == qv4[g][2];
-            if (p.r > 3) ok = ok && rv.w == qv4[g][3];
-            if (ok) m |= 1 << g;
-          }
-        } else {
+      for (int ps = 0; ps < kPasses; ++ps) {
+        bool ok = true;
+        if (p.r > 0) ok = ok && rv[ps].x == qmine[0];
+        if (p.r > 1) ok = ok && rv[ps].y == qmine[1];
+        if (p.r > 2) ok = ok && rv[ps].z == qmine[2];
+        if (p.r > 3) ok = ok && rv[ps].w == qmine[3];
+        hit[ps] = ok;
+      }
+    } else {
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const int32_t* rv = p.router + phys[c] * p.rs0 + (h0 + g) * p.rs1;
-            bool ok = true;
-            for (int lev = 0; lev < p.r; ++lev) {
-              if (rv[lev * p.rs2] != qroute[g][lev]) {
-                ok = false;
-                break;
-              }
-            }
-            if (ok) m |= 1 << g;
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
+        const int32_t* rv = p.router + ph * p.rs0 + (h0 + gl) * p.rs1;
+        bool ok = true;
+        for (int lev = 0; lev < p.r; ++lev) {
+          if (rv[lev * p.rs2] != qroute[gl][lev]) {
+            ok = false;
+            break;
           }
         }
+        hit[ps] = ok;
       }
-      mask[c] = m;
     }
-    int nsel = 0;
 #pragma unroll
-    for (int c = 0; c < kChunksPerRange; ++c) {
-      const int l = r0 + c * kDecThreads + tid;
-      const uint64_t bal = __ballot(mask[c] != 0);
-      if (lane == 0) wave_count[wave] = __popcll(bal);
-      __syncthreads();
-      int base = nsel, tot = 0;
-#pragma unroll
-      for (int w = 0; w < kDecWaves; ++w) {
-        const int cw = wave_count[w];
-        if (w < wave) base += cw;
-        tot += cw;
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int l = r0 + ps * kPagesPerPass + pslot;
+      const bool valid = l < r1 && phys[ps] >= 0 && phys[ps] < p.P;
+      const bool forced = (p.sink && l == 0) || (p.local > 0 && l >= n - p.local);
+      const uint64_t bal = __ballot(valid && (forced || hit[ps]));
+      if (gl == 0) {
+        const int m = static_cast<int>((bal >> (lane - gl)) & ((1u << G) - 1u));
+        page_mask[ps * kPagesPerPass + pslot] = static_cast<uint8_t>(m);
+        page_phys[ps * kPagesPerPass + pslot] = phys[ps];
       }
-      if (mask[c] != 0) {
-        const int pos = base + static_cast<int>(lanes_below(bal));
-        sel_phys[pos] = phys[c];
-        sel_meta[pos] = (l - r0) | (mask[c] << 16);
-      }
-      nsel += tot;
-      __syncthreads();
     }
+    __syncthreads();
+    // ---- phase A2: compact selected pages in ascending logical order -----------
+    const int cnt = r1 - r0;
+    int mm[kPagesPerThread];
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < kPagesPerThread; ++j) {
+      const int l = tid * kPagesPerThread + j;
+      mm[j] = l < cnt ? page_mask[l] : 0;
+      mine += mm[j] != 0;
+    }
+    int incl = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
+    }
+    if (lane == 63) wave_count[wave] = incl;
+    __syncthreads();
+    int pos = incl - mine, nsel = 0;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+      const int cw = wave_count[w];
+      if (w < wave) pos += cw;
+      nsel += cw;
+    }
+#pragma unroll
+    for (int j = 0; j < kPagesPerThread; ++j) {
+      if (mm[j] != 0) {
+        const int l = tid * kPagesPerThread + j;
+        sel_phys[pos] = page_phys[l];
+        sel_meta[pos] = l | (mm[j] << 16);
+        ++pos;
+      }
+    }
+    __syncthreads();
 
     // ---- phase B: gather + attend the selected pages ----------------------------
     // fetch() loads K and V rows of one page into a register buffer; attend()

@@ -10,16 +10,19 @@
 //
 // Two kernels:
 //  * prefill_mfma_kernel — bf16/fp16, D in {32, 64, 128}, route_block % 32 == 0.
-//    A workgroup of NW waves owns BM = 32*NW query rows of one route block.
-//    Each wave computes S^T = K Q^T on 32x32x16 MFMA tiles, so lane (i + 32h)
-//    holds 16 keys of query i per tile: row max / row sum need one exchange
-//    with lane ^ 32, and the O^T = V^T P^T accumulator is rescaled with one
-//    per-lane scalar. K/V sub-tiles of BN keys are double-buffered in LDS:
-//    K rows with an XOR swizzle on 16-byte chunks, V as 4-key "quads"
-//    (entry [quad][d] = the 4 keys' values of column d) so each MFMA operand
-//    is two conflict-free 8-byte LDS reads. Workgroup ids are remapped so
-//    that each XCD works on a contiguous range of heads (shared K/V blocks
-//    hit that XCD's L2).
+//    A workgroup of NW waves owns BM = 32*NW query rows of one route block;
+//    Q stays in registers as MFMA operands. Each wave computes S^T = K Q^T on
+//    32x32x16 MFMA tiles, so lane (i + 32h) holds 16 keys of query i per
+//    tile: row max / row sum need one exchange with lane ^ 32
+//    (permlane32_swap), and the O^T = V^T P^T accumulator is rescaled with a
+//    per-lane scalar, lazily (only when a row max grows by more than 2^8).
+//    K/V tiles of BN = 32 keys stream through a 4-stage LDS ring filled by
+//    direct-to-LDS loads (global_load_lds_dwordx4, no VGPR staging); rows
+//    are stored with an XOR swizzle on 16-byte chunks, K is read as
+//    row-major 16-byte MFMA operands and V through ds_read_b64_tr_b16
+//    (transposing reads), both bank-conflict free. Workgroup ids are
+//    remapped so that each XCD works on a contiguous range of heads (shared
+//    K/V blocks hit that XCD's L2).
 //  * prefill_generic_kernel — any of fp32/bf16/fp16, D power of two in
 //    [16, 256], any route block: 16 lanes per query row, fp32 FMA math, used
 //    for fp32 inputs (true fp32, no TF32 shortcut) and shapes the MFMA path
