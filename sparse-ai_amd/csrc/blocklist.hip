@@ -9,9 +9,10 @@
 //   * the k-th active key block of a row goes to slot k, slots >= count are 0
 //     (block_list.py:263-278).
 //
-// Design: one workgroup = 4 waves handles 64 consecutive query-block rows of
-// one (z, h). The NB key codes of that head are computed once into LDS; each
-// wave then walks its rows 64 key blocks at a time: one predicate per lane,
+// Design: one workgroup = 4 waves handles 4*R consecutive query-block rows of
+// one (z, h), R = rows per wave (1..16, as few as keeps ~4096 waves busy).
+// The NB key codes of that head are computed into LDS; each wave then walks
+// its rows 64 key blocks at a time: one predicate per lane,
 // a wave ballot, and mbcnt (popcount of the ballot below the lane) gives
 // every active lane its output slot. Padding zeros are written by the same
 // kernel, so the output needs no memset.
@@ -21,8 +22,8 @@ namespace sa {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kRowsPerWave = 16;
-constexpr int kRowsPerGroup = kWaves * kRowsPerWave;
+constexpr int kMaxRowsPerWave = 16;
+constexpr long long kTargetWaves = 4096;  // enough waves to fill 256 CUs
 constexpr int kMaxNB = 8192;  // codes of one head live in LDS: 8192 * 8 B = 64 KB
 
 enum MatchMode { kCodes = 0, kElementwise = 1, kMask = 2 };
@@ -41,6 +42,7 @@ struct BLParams {
   int cols;
   int32_t* counts;
   int groups_per_head;
+  int rows_per_wave;
 };
 
 template <typename IdT>
@@ -81,8 +83,8 @@ __global__ __launch_bounds__(kWaves * 64) void blocklist_kernel(BLParams p) {
 
   const int wave = threadIdx.x / 64;
   const int lane = threadIdx.x % 64;
-  const int row0 = group * kRowsPerGroup + wave * kRowsPerWave;
-  for (int r = 0; r < kRowsPerWave; ++r) {
+  const int row0 = (group * kWaves + wave) * p.rows_per_wave;
+  for (int r = 0; r < p.rows_per_wave; ++r) {
     const int qb = row0 + r;
     if (qb >= NB) break;
     const int64_t row = static_cast<int64_t>(zh) * NB + qb;
@@ -137,7 +139,12 @@ int launch(BLParams& p, int mode, int id_dtype, hipStream_t stream) {
   if (!p.counts) return fail(SA_EINVAL, "counts must not be NULL");
   const long long rows_total = static_cast<long long>(p.Z) * p.H * p.NB;
   if (rows_total == 0) return SA_OK;
-  p.groups_per_head = (p.NB + kRowsPerGroup - 1) / kRowsPerGroup;
+  // Rows per wave: as few as keeps ~kTargetWaves waves busy (each workgroup
+  // recomputes its head's NB codes, a cached read of NB * TD ids).
+  long long rpw = (rows_total + kTargetWaves - 1) / kTargetWaves;
+  p.rows_per_wave = static_cast<int>(rpw < 1 ? 1 : (rpw > kMaxRowsPerWave ? kMaxRowsPerWave : rpw));
+  const int rows_per_group = kWaves * p.rows_per_wave;
+  p.groups_per_head = (p.NB + rows_per_group - 1) / rows_per_group;
   const long long grid = static_cast<long long>(p.Z) * p.H * p.groups_per_head;
   if (grid > 0x7fffffffLL) return fail(SA_EINVAL, "too many rows");
   const size_t lds = mode == kCodes ? static_cast<size_t>(p.NB) * sizeof(uint64_t) : 0;
