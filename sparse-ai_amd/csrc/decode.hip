@@ -22,7 +22,7 @@
 //     their loads back to back;
 //   phase A2 — the selected pages are compacted into LDS in ascending logical
 //     order (per-thread counts, wave prefix sum, per-wave offsets);
-//   phase B — the 4 waves take selected pages round-robin with up to 3 pages
+//   phase B — the 4 waves take selected pages round-robin with up to 2 pages
 //     in flight per wave (register ring indexed by compile-time constants).
 //     16 lanes cover one token row of D elements (one vector load each) and
 //     the 4 lane groups take tokens g, g+4, ... of the page; QK uses packed
@@ -138,7 +138,8 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t ballot) {
 }
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(G * D <= 512 ? 2 : 1)))
+void decode_kernel(DecParams p) {
   constexpr int DPL = D / 16;
   // Phase A layout: G consecutive lanes share one page (lane j reads head j's
   // routing vector, so a page's G vectors are one contiguous 16*G-byte read);
@@ -167,23 +168,28 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
   const int b = bk / p.Hkv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h0 = kvh * G;
+  const int gl = tid % G;       // head (within the group) whose routing vector this lane checks
+  const int pslot = tid / G;    // page slot within a pass
+
+  // A memory round trip costs microseconds under load, so every load that
+  // does not depend on another is issued before the first wait: the first
+  // range's block-table entries (split 0 starts at page 0 whatever the
+  // context length), the context length, the query routing vectors and Q.
+  const bool prefetched = split == 0 && p.max_pages > 0;
+  int phys0[kPasses];
+  if (prefetched) {
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int l = min(ps * kPagesPerPass + pslot, p.max_pages - 1);
+      phys0[ps] = p.bt[b * p.bts0 + l * p.bts1];
+    }
+  }
   const int ctx = p.ctx[b];
   int n = ctx > 0 ? (ctx + p.PS - 1) / p.PS : 0;
   if (n > p.max_pages) n = p.max_pages;  // block-table bound (memory safety)
   // This split's logical page range [pa, pz).
   const int pa = static_cast<int>((static_cast<long long>(n) * split) / p.splits);
   const int pz = static_cast<int>((static_cast<long long>(n) * (split + 1)) / p.splits);
-
-  for (int i = tid; i < G * p.r; i += kDecThreads) {
-    const int g = i / p.r, lev = i % p.r;
-    qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
-  }
-  __syncthreads();
-  const int gl = tid % G;       // head (within the group) whose routing vector this lane checks
-  const int pslot = tid / G;    // page slot within a pass
-  int qmine[4];                 // this lane's head's first four query levels (vector path)
-#pragma unroll
-  for (int lev = 0; lev < 4; ++lev) qmine[lev] = lev < p.r ? qroute[gl][lev] : 0;
 
   const int grp = lane >> 4, sub = lane & 15;
   constexpr int QW = RowRegs<T, DPL>::kWords;
@@ -204,17 +210,32 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
     m_s[g] = -INFINITY;
     l_s[g] = 0.f;
   }
+  for (int i = tid; i < G * p.r; i += kDecThreads) {
+    const int g = i / p.r, lev = i % p.r;
+    qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
+  }
+  __syncthreads();
+  int qmine[4];                 // this lane's head's first four query levels (vector path)
+#pragma unroll
+  for (int lev = 0; lev < 4; ++lev) qmine[lev] = lev < p.r ? qroute[gl][lev] : 0;
 
   for (int r0 = pa; r0 < pz; r0 += kRange) {
     const int r1 = min(pz, r0 + kRange);
     // ---- phase A1: block table + routing vectors -> per-page head mask ---------
     // All loads are unconditional (indices clamped into range) so they issue
     // back to back; out-of-range results are discarded afterwards.
+    // The prefetched first range holds entries for pages past r1 as well:
+    // their routing vectors are not loaded (and the pages are never selected).
+    const bool use_pre = prefetched && r0 == 0;
     int phys[kPasses];
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps) {
-      const int l = min(r0 + ps * kPagesPerPass + pslot, r1 - 1);
-      phys[ps] = p.bt[b * p.bts0 + l * p.bts1];
+      if (use_pre) {
+        phys[ps] = phys0[ps];
+      } else {
+        const int l = min(r0 + ps * kPagesPerPass + pslot, r1 - 1);
+        phys[ps] = p.bt[b * p.bts0 + l * p.bts1];
+      }
     }
     bool hit[kPasses];
     if (p.vec_router) {
@@ -222,7 +243,9 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
-        rv[ps] = *reinterpret_cast<const int4*>(p.router + ph * p.rs0 + (h0 + gl) * p.rs1);
+        const bool need = !use_pre || ps * kPagesPerPass + pslot < r1;
+        rv[ps] = need ? *reinterpret_cast<const int4*>(p.router + ph * p.rs0 + (h0 + gl) * p.rs1)
+                      : int4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
@@ -238,8 +261,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
         const int32_t* rv = p.router + ph * p.rs0 + (h0 + gl) * p.rs1;
-        bool ok = true;
-        for (int lev = 0; lev < p.r; ++lev) {
+        bool ok = !use_pre || ps * kPagesPerPass + pslot < r1;
+        for (int lev = 0; ok && lev < p.r; ++lev) {
           if (rv[lev * p.rs2] != qroute[gl][lev]) {
             ok = false;
             break;
@@ -353,9 +376,10 @@ __global__ __launch_bounds__(kDecThreads) void decode_kernel(DecParams p) {
       // Fetch indices past the end are clamped to the wave's last page (a
       // reread that hits cache), so every iteration issues the same loads and
       // the load counter waits stay static.
-      // Pages in flight per wave: 3 when a page costs <= 32 registers per
-      // lane (16-bit D <= 128, fp32 D <= 64), fewer for wider rows.
-      constexpr int kDecBufs = 8 * QW <= 32 ? 3 : (8 * QW <= 64 ? 2 : 1);
+      // Pages in flight per wave: 3 when a page costs <= 16 registers per
+      // lane (16-bit D <= 64, fp32 D <= 32), 2 up to 32 registers, else 1
+      // (two resident workgroups per CU matter more than a deeper ring).
+      constexpr int kDecBufs = 8 * QW <= 16 ? 3 : (8 * QW <= 32 ? 2 : 1);
       if (wave < nsel) {
         const int last = wave + ((nsel - 1 - wave) / kDecWaves) * kDecWaves;
         Rows kx[kDecBufs], vx[kDecBufs];

@@ -81,7 +81,7 @@ template <> __device__ __forceinline__ float round_to<f16_t>(float x) {
   return f16_bits_to_float(float_to_f16_bits(x));
 }
 
-constexpr int kListCache = 1024;  // MFMA path: a row's list (<= 1024 blocks) lives in LDS
+constexpr int kListSeg = 256;  // MFMA path: list entries staged in LDS at a time
 
 // ============================================================================
 // Generic kernel: 16 query rows per workgroup, 16 lanes per row.
@@ -214,21 +214,39 @@ __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "m
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 #define SA_LDS __attribute__((address_space(3)))
 
-// Direct-to-LDS load of 16 bytes per lane: lane L's bytes land at LDS
+// Direct-to-LDS loads of 16 bytes per lane: lane L's bytes land at LDS
 // address lds_addr + 16 L. Issued through inline asm so that the compiler
-// does not track it: its own wait insertion would otherwise drain every
+// does not track them: its own wait insertion would otherwise drain every
 // in-flight load before any LDS read. The kernel waits for these loads with
 // explicit vmcnt counts before the barrier that publishes a stage.
+//   dma16:   64-bit per-lane address.
+//   dma16_s: uniform 64-bit base in SGPRs + 32-bit per-lane byte offset.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds_addr), "v"(src) : "memory", "m0");
 }
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr), "v"(off), "s"(base) : "memory", "m0");
+}
 
-template <typename T, int D, int NW, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+// Wait until at most `ahead` pipeline tiles (LPW loads each) are in flight:
+// `ahead` is the number of tiles issued after the one about to be computed.
+template <int LPW, int MAXA>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+  static_assert(MAXA >= 1 && MAXA <= 3, "pipeline depth");
+  if (MAXA >= 3 && ahead >= 3) wait_vmcnt<3 * LPW>();
+  else if (MAXA >= 2 && ahead >= 2) wait_vmcnt<2 * LPW>();
+  else if (ahead >= 1) wait_vmcnt<LPW>();
+  else wait_vmcnt<0>();
+}
+
+// S: pipeline stages (K+V tiles of BN keys; S - 1 in flight while one is
+// computed). WPE: waves per SIMD the register budget is sized for.
+template <typename T, int D, int NW, bool CAUSAL, int S, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void prefill_mfma_kernel(FwdParams p) {
   constexpr int BN = 32;               // keys per pipeline stage
-  constexpr int S = 4;                 // pipeline stages (tiles in flight: S - 1)
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;
   constexpr int CPR = D / 8;           // 16-byte chunks per row
@@ -241,13 +259,14 @@ void prefill_mfma_kernel(FwdParams p) {
   constexpr int LPW = 2 * NKI / NW;    // loads per wave per stage (K and V)
   constexpr int RSH = D == 128 ? 0 : (D == 64 ? 1 : 2);  // log2(rows per 256 B)
   static_assert((2 * NKI) % NW == 0, "loads must split evenly over waves");
+  static_assert(S >= 3 && S <= 4, "pipeline stages");
   // O is rescaled only when a row maximum grows by more than this (log2
   // units); until then p = exp2(s - m_ref) <= 2^8.
   constexpr float kRescale = 8.f;
 
   __shared__ __attribute__((aligned(1024))) char stage_lds[S * STAGEB];
-  __shared__ int32_t list_lds[kListCache];
-  __shared__ float bias_lds[kListCache];
+  __shared__ int32_t list_lds[kListSeg];
+  __shared__ float bias_lds[kListSeg];
 
   const int work = xcd_remap(blockIdx.x, p.total_wg);
   const int zh = work / p.mtiles;
@@ -259,16 +278,11 @@ void prefill_mfma_kernel(FwdParams p) {
   const int count = min(max(p.counts[row], 0), p.max_count);
   const int32_t* list = p.lists + row * p.max_count;
   const int spb = p.RB / BN;
-  const int total = count * spb;
+  const int lspb = __builtin_ctz(spb);   // spb = route_block / 32 is a power of two
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  for (int t = tid; t < count; t += NT) {
-    list_lds[t] = list[t];
-    if (p.sb) bias_lds[t] = load_bias(p, z, h, qb, t);
-  }
-  __syncthreads();
   const int li = lane & 31, kh = lane >> 5;
   const int qw0 = m0 + wave * 32;
   const int qpos = qw0 + li;
@@ -307,7 +321,8 @@ void prefill_mfma_kernel(FwdParams p) {
 
   // Direct-to-LDS loads: load i of this wave fills 1-KB block `blk` of the
   // K (isk) or V tile: lane L writes slot 64 blk + L = (row, position), and
-  // fetches the global chunk that belongs at that position.
+  // fetches the global chunk that belongs at that position. Whether a load
+  // targets K or V depends on the wave only (uniform).
   uint32_t goff[LPW];   // byte offset of the lane's chunk from the tile's first row
   int grow[LPW];        // the lane's row inside the tile
 #pragma unroll
@@ -320,31 +335,36 @@ void prefill_mfma_kernel(FwdParams p) {
     grow[i] = r;
     goff[i] = __umul24(static_cast<uint32_t>(r), isk ? ksb : vsb) + 16u * cc;
   }
-  // Tile m covers keys list[m / spb] * RB + (m % spb) * BN .. +BN; spb is a
-  // power of two (route_block / 32).
-  const int lspb = __builtin_ctz(spb);
-  auto tile_key0 = [&](int m) { return list_lds[m >> lspb] * p.RB + (m & (spb - 1)) * BN; };
   const uint32_t lds_base = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SA_LDS char*)stage_lds));
+  // Issues the K and V loads of the tile whose first key is key0 into stage stg.
   auto issue = [&](int key0, int stg) {
-    const bool full = key0 >= 0 && key0 + BN <= N;
+    if (key0 >= 0 && key0 + BN <= N) {
+      // Whole tile in range: one scalar base per tile, per-lane 32-bit offsets.
+      const char* kt = kbase + static_cast<size_t>(key0) * ksb;
+      const char* vt = vbase + static_cast<size_t>(key0) * vsb;
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) {
-      const int q = wave * LPW + i;
-      const bool isk = q < NKI;
-      const char* gb = isk ? kbase : vbase;
-      const uint32_t rs = isk ? ksb : vsb;
-      const char* src;
-      if (full) {
-        src = gb + static_cast<size_t>(key0) * rs + goff[i];
-      } else {
-        // Rows outside [0, N) read a valid row: their scores are masked to
-        // -inf, so p = 0 and the data never reaches the output.
-        const uint32_t rr = static_cast<uint32_t>(min(max(key0 + grow[i], 0), N - 1));
-        src = gb + __umul24(rr, rs) + (goff[i] - __umul24(static_cast<uint32_t>(grow[i]), rs));
+      for (int i = 0; i < LPW; ++i) {
+        const int q = wave * LPW + i;
+        const bool isk = q < NKI;
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(
+            lds_base + stg * STAGEB + (isk ? 0 : TILEB) + (isk ? q : q - NKI) * 1024);
+        dma16_s(isk ? kt : vt, goff[i], dst);
       }
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(
-          lds_base + stg * STAGEB + (isk ? 0 : TILEB) + (isk ? q : q - NKI) * 1024);
-      dma16(src, dst);
+    } else {
+      // Rows outside [0, N) read a valid row: their scores are masked to
+      // -inf, so p = 0 and the data never reaches the output.
+#pragma unroll
+      for (int i = 0; i < LPW; ++i) {
+        const int q = wave * LPW + i;
+        const bool isk = q < NKI;
+        const char* gb = isk ? kbase : vbase;
+        const uint32_t rs = isk ? ksb : vsb;
+        const uint32_t rr = static_cast<uint32_t>(min(max(key0 + grow[i], 0), N - 1));
+        const char* src = gb + __umul24(rr, rs) + (goff[i] - __umul24(static_cast<uint32_t>(grow[i]), rs));
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(
+            lds_base + stg * STAGEB + (isk ? 0 : TILEB) + (isk ? q : q - NKI) * 1024);
+        dma16(src, dst);
+      }
     }
   };
 
@@ -374,18 +394,13 @@ void prefill_mfma_kernel(FwdParams p) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16_t{};
   float m_i = -INFINITY, l_i = 0.f;
-  int cur_t = -1;
-  float bias = 0.f;
 
+  // Folds tile n (first key key0, held in stage stg) into the running state.
   auto compute = [&](int n, int key0, int stg) {
-    const int t = n >> lspb;
-    if (p.sb && t != cur_t) {
-      bias = bias_lds[t];
-      cur_t = t;
-    }
     const bool skip = qw0 >= N || static_cast<unsigned>(key0) >= static_cast<unsigned>(N) ||
                       (CAUSAL && key0 > qw0 + 31);
     if (skip) return;
+    const float bias = bias_lds[n >> lspb];
     char* sbase = stage_lds + stg * STAGEB;
 
     // S^T = K Q^T (raw dot products); register v of lane (i + 32 h) holds key
@@ -393,14 +408,9 @@ void prefill_mfma_kernel(FwdParams p) {
     u32x4_t ka[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) ka[s] = *reinterpret_cast<const u32x4_t*>(sbase + k_rd[s]);
-    // Two independent accumulation chains halve the dependent-MFMA latency.
-    f32x16_t st = f32x16_t{}, st2 = f32x16_t{};
+    f32x16_t st = f32x16_t{};
 #pragma unroll
-    for (int s = 0; s < KS; s += 2) {
-      st = Mma<T>::mma(ka[s], qf[s], st);
-      st2 = Mma<T>::mma(ka[s + 1], qf[s + 1], st2);
-    }
-    st += st2;
+    for (int s = 0; s < KS; ++s) st = Mma<T>::mma(ka[s], qf[s], st);
 
     const bool need_mask = key0 + BN > N || (CAUSAL && key0 + BN - 1 > qw0);
     if (need_mask) {
@@ -457,45 +467,57 @@ void prefill_mfma_kernel(FwdParams p) {
     }
   };
 
-  // No compiler-visible load may be outstanding once the pipeline runs (the
-  // explicit vmcnt waits below count only the pipeline's own loads).
-  __builtin_amdgcn_s_waitcnt(0);
-  // Pipeline: tiles n+1 .. n+S-2 stay in flight while tile n is computed;
-  // tile n+S-1 is issued into the stage tile n-1 used, once every wave has
-  // passed the barrier that follows tile n-1's compute.
-  // Key offsets of the tiles held by each stage live in registers; the list
-  // entry of the next tile to issue is read one iteration ahead.
-  int key_of[S];
-#pragma unroll
-  for (int st0 = 0; st0 < S - 1; ++st0) {
-    key_of[st0] = st0 < total ? tile_key0(st0) : 0;
-    if (st0 < total) issue(key_of[st0], st0);
-  }
-  int next_key = S - 1 < total ? tile_key0(S - 1) : 0;
-  int n = 0;
-  auto step = [&](auto stg_c) {
-    constexpr int stg = decltype(stg_c)::value;
-    if (n >= total) return;
-    const int after = total - 1 - n;   // tiles issued after tile n (capped at S - 2)
-    if (after >= 2) wait_vmcnt<2 * LPW>();
-    else if (after == 1) wait_vmcnt<LPW>();
-    else wait_vmcnt<0>();
-    barrier_only();
-    if (n + S - 1 < total) {
-      constexpr int nst = (stg + S - 1) % S;
-      key_of[nst] = next_key;
-      issue(next_key, nst);
-      if (n + S < total) next_key = tile_key0(n + S);
+  // The row's list is walked in segments of at most kListSeg blocks, each
+  // staged in LDS (with its soft-bias values, zero when there is none). Tile
+  // m of a segment covers keys list[m / spb] * RB + (m % spb) * BN .. +BN.
+  for (int seg = 0; seg < count; seg += kListSeg) {
+    const int seg_n = min(count - seg, kListSeg);
+    if (seg > 0) __syncthreads();   // every wave is done with the previous segment
+    for (int t = tid; t < seg_n; t += NT) {
+      list_lds[t] = list[seg + t];
+      bias_lds[t] = p.sb ? load_bias(p, z, h, qb, seg + t) : 0.f;
     }
-    compute(n, key_of[stg], stg);
-    ++n;
-  };
-  static_assert(S == 4, "the loop below is unrolled for 4 stages");
-  while (n < total) {
-    step(std::integral_constant<int, 0>{});
-    step(std::integral_constant<int, 1>{});
-    step(std::integral_constant<int, 2>{});
-    step(std::integral_constant<int, 3>{});
+    __syncthreads();
+    // No compiler-visible load may be outstanding once the pipeline runs (the
+    // explicit vmcnt waits below count only the pipeline's own loads).
+    __builtin_amdgcn_s_waitcnt(0);
+    const int total = seg_n * spb;
+    auto tile_key0 = [&](int m) { return list_lds[m >> lspb] * p.RB + (m & (spb - 1)) * BN; };
+
+    // Pipeline: tiles n+1 .. n+S-2 stay in flight while tile n is computed;
+    // tile n+S-1 is issued into the stage tile n-1 used, once every wave has
+    // passed the barrier that follows tile n-1's compute. Key offsets of the
+    // tiles held by each stage live in registers; the list entry of the next
+    // tile to issue is read one step ahead.
+    int key_of[S];
+#pragma unroll
+    for (int st0 = 0; st0 < S - 1; ++st0) {
+      key_of[st0] = st0 < total ? tile_key0(st0) : 0;
+      if (st0 < total) issue(key_of[st0], st0);
+    }
+    key_of[S - 1] = 0;
+    int next_key = S - 1 < total ? tile_key0(S - 1) : 0;
+    int n = 0;
+    auto step = [&](auto stg_c) {
+      constexpr int stg = decltype(stg_c)::value;
+      if (n >= total) return;
+      wait_tiles<LPW, S - 2>(total - 1 - n);
+      barrier_only();
+      if (n + S - 1 < total) {
+        constexpr int nst = (stg + S - 1) % S;
+        key_of[nst] = next_key;
+        issue(next_key, nst);
+        if (n + S < total) next_key = tile_key0(n + S);
+      }
+      compute(n, key_of[stg], stg);
+      ++n;
+    };
+    while (n < total) {
+      step(std::integral_constant<int, 0>{});
+      step(std::integral_constant<int, 1>{});
+      if constexpr (S > 2) step(std::integral_constant<int, 2>{});
+      if constexpr (S > 3) step(std::integral_constant<int, 3>{});
+    }
   }
 
   const float l_tot = l_i + __shfl_xor(l_i, 32);
@@ -535,23 +557,31 @@ int launch_generic(FwdParams& p, int D, hipStream_t stream) {
   return check_launch("block-sparse prefill (generic) kernel");
 }
 
-template <typename T, int D, int NW>
+template <typename T, int D, int NW, int S, int WPE>
 void launch_mfma_shape(FwdParams& p, hipStream_t stream) {
   p.mtiles = (p.N + NW * 32 - 1) / (NW * 32);
   p.total_wg = p.Z * p.H * p.mtiles;
   dim3 g(p.total_wg), b(NW * 64);
   if (p.is_causal)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, true>), g, b, 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, true, S, WPE>), g, b, 0, stream, p);
   else
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, false>), g, b, 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, false, S, WPE>), g, b, 0, stream, p);
+}
+
+// Three pipeline stages (48 KB of LDS at D = 128) and a register budget of
+// three waves per SIMD: three workgroups share a CU, so one workgroup's
+// prologue / epilogue latency overlaps the others' MFMA work.
+template <typename T, int D, int NW>
+void launch_mfma_variant(FwdParams& p, hipStream_t stream) {
+  launch_mfma_shape<T, D, NW, 3, 3>(p, stream);
 }
 
 template <typename T, int D>
 int launch_mfma_d(FwdParams& p, hipStream_t stream) {
   const int RB = p.RB;
-  if (RB % 128 == 0) launch_mfma_shape<T, D, 4>(p, stream);
-  else if (RB == 64) launch_mfma_shape<T, D, 2>(p, stream);
-  else launch_mfma_shape<T, D, 1>(p, stream);  // RB == 32
+  if (RB % 128 == 0) launch_mfma_variant<T, D, 4>(p, stream);
+  else if (RB == 64) launch_mfma_variant<T, D, 2>(p, stream);
+  else launch_mfma_variant<T, D, 1>(p, stream);  // RB == 32
   return check_launch("block-sparse prefill (MFMA) kernel");
 }
 
@@ -629,7 +659,7 @@ extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, 
   const bool offs_ok = N < (1 << 24) && max_rs < (1 << 24) &&
                        static_cast<long long>(N) * max_rs < (1LL << 32);
   const bool mfma_ok = dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128) &&
-                       route_block >= 32 && rows_ok && offs_ok && max_count <= kListCache;
+                       route_block >= 32 && rows_ok && offs_ok;
   const long long wg = static_cast<long long>(Z) * H * ((N + 15) / 16);
   if (wg > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
 

@@ -87,6 +87,37 @@ def test_multi_split_long_sequences():
         assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
 
 
+@pytest.mark.parametrize("B,max_len", [(300, 200), (37, 3000)])
+def test_many_sequences_balanced_slices(B, max_len):
+    # equal unit slices over 512 workgroups cut many segments: zero-length sequences
+    # interspersed, every sequence checked against the oracle
+    g = torch.Generator().manual_seed(B)
+    lens = torch.randint(0, max_len, (B,), generator=g)
+    lens[::7] = 0
+    lens[1] = max_len
+    args = make(B=B, H=4, Hkv=2, D=32, page=8, pages=max(64, -(-max_len // 8) + 8), TD=3, p=2,
+                lens=[int(x) for x in lens], dtype=torch.float32, seed=B + 1)
+    for kw in (dict(req_depth=1, local_blocks=2, sink_block=True), dict(req_depth=3), dict(req_depth=0)):
+        out = run(args, **kw)
+        ref = oracle(args, torch.float32, **kw)
+        assert np.abs(out.cpu().numpy() - ref).max() <= 1e-5, kw
+        assert torch.all(out[lens == 0] == 0)
+
+
+def test_more_sequences_than_balanced_limit():
+    # > 4096 sequences: one workgroup per (sequence, kv head), no workspace
+    B = 4100
+    g = torch.Generator().manual_seed(5)
+    lens = [int(x) for x in torch.randint(0, 40, (B,), generator=g)]
+    args = make(B=B, H=4, Hkv=2, D=32, page=16, pages=32, TD=2, p=2, lens=lens, dtype=torch.float32, seed=6,
+                max_pages=3)
+    out = run(args, req_depth=1, local_blocks=1, sink_block=True)
+    sub = list(range(0, B, 97))
+    sargs = [a[sub] if i in (0, 3, 4, 6) else a for i, a in enumerate(args)]
+    ref = oracle(sargs, torch.float32, req_depth=1, local_blocks=1, sink_block=True)
+    assert np.abs(out[sub].cpu().numpy() - ref).max() <= 1e-5
+
+
 def test_out_of_range_pages_are_skipped():
     args = make(B=2, H=4, Hkv=4, D=32, page=8, pages=10, TD=2, p=2, lens=[70, 40], dtype=torch.float32,
                 seed=3)
