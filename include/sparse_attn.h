@@ -171,6 +171,24 @@ int sa_sparse_paged_decode(const void* q, const void* k_cache, const void* v_cac
                            const int64_t* o_strides, void* workspace, size_t workspace_bytes,
                            int dtype, void* stream);
 
+/*
+ * Route-block majority vote of the surgery caller.
+ * Replaces: the per-level majority vote of token argmax branches in
+ *   SurgicalLlamaAttention._block_list_prefill
+ *   (src/llama_surgery/surgery.py:543-547; with route_block = 1, the direct
+ *   block routing of :536-541).
+ *
+ * assign      (B, H, S, L, p) branch scores, element type dtype (F32/BF16/F16),
+ *             strides[5].
+ * out         (B, H, ceil(S / route_block), r) int32 contiguous: for block i
+ *             and level l < r, the branch chosen by the most tokens of the
+ *             block (token vote = argmax over p, first maximum on ties; block
+ *             winner = lowest branch id on ties). Tokens >= S do not vote.
+ * Limits: p <= 64, r <= 32 (r <= L).
+ */
+int sa_route_block_vote(const void* assign, int dtype, const int64_t* strides, int B, int H, int S,
+                        int L, int p, int r, int route_block, int32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

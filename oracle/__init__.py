@@ -14,8 +14,11 @@ Modules:
   attention  — token masks and masked-dense attention (out and LSE), float64
                numpy, plus the fp32 torch variant timed as the CPU baseline.
   decode     — sparse paged decode reference (GQA by head grouping).
+  surgery    — the surgery caller's route-block majority vote and its
+               allowed-key statistics.
 
 Parity pinning: see the header of each module for the checks that pin it
 (known-answer tests from the reference's own tests, closed forms, brute
-force on tiny inputs). The reference ships no golden vectors for this path.
+force on tiny inputs). The reference ships no golden vectors for this path;
+tests/golden/ holds this build's own fixtures (written from this oracle).
 """

@@ -3,8 +3,10 @@
 Drop-in for the kernel API of the reference package ``src/ultrametric``
 (__init__.py:24-36 and kernel_decode.py): the same function names and
 signatures, backed by hand-written HIP kernels for gfx950 in libsparseattn.so.
-The reference's training model, topology routers, layers and legacy kernels
-are outside this package's scope.
+``surgery`` adds the model-side caller (the route-block vote and causal
+prefill of src/llama_surgery/surgery.py:521-601). The reference's training
+model, topology routers, layers and legacy kernels are outside this
+package's scope.
 """
 
 from .block_list import (
@@ -19,6 +21,7 @@ from .block_list import (
 )
 from .kernel import block_sparse_attention, routing_to_block_indices
 from .kernel_decode import ultrametric_decode
+from .surgery import block_list_prefill, route_block_vote
 
 __all__ = [
     "HAS_TRITON",
@@ -32,4 +35,6 @@ __all__ = [
     "block_sparse_attention",
     "routing_to_block_indices",
     "ultrametric_decode",
+    "route_block_vote",
+    "block_list_prefill",
 ]

@@ -40,6 +40,7 @@ _SIGNATURES = {
     "sa_sparse_paged_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                     _I, _I, _I, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
                                     _P, ctypes.c_size_t, _I, _P]),
+    "sa_route_block_vote": (_I, [_P, _I, _I64P, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -1,0 +1,107 @@
+"""Surgery-side block routing and prefill (the model caller of the hot path).
+
+Mirrors ``SurgicalLlamaAttention._block_list_prefill``
+(src/llama_surgery/surgery.py:521-601), the only model-side caller of the
+block-list kernel in the reference, as free functions over the same inputs
+(the reference reads them from its module and config):
+
+* ``route_block_vote`` — one routing vector per route block: per level, the
+  branch most of the block's tokens pick (token choice = argmax over the p
+  branch scores, first maximum on ties; block winner = lowest branch id on
+  ties; surgery.py:543-547), or with ``route_block = 1`` the per-row argmax of
+  direct block assignments (surgery.py:536-541). One HIP kernel
+  (``sa_route_block_vote``) replaces the reference's argmax / one_hot / pad /
+  view / sum / argmax chain.
+* ``block_list_prefill`` — the causal prefill: vote, sync-free list build with
+  causal + sink + ceil(local_window / route_block) local blocks and
+  arity = p (surgery.py:550-564), then ``block_list_attention`` with the
+  caller's softmax scale (surgery.py:599-601). K / V may carry fewer heads
+  (GQA): the kernel indexes kv head h // (H / H_kv) instead of materialising
+  ``repeat_kv`` (surgery.py:77-86). Optional statistics follow
+  surgery.py:589-595.
+
+The reference's straight-through soft-bias gradient (surgery.py:566-588)
+needs the block-list backward, which this build does not provide: a call
+that requires gradients raises RuntimeError (as block_list_attention does).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _native as nat
+from .block_list import block_list_attention, build_block_lists
+
+__all__ = ["route_block_vote", "block_list_prefill", "local_blocks_of"]
+
+_SCORE_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def local_blocks_of(local_window: int, route_block: int) -> int:
+    """Local band in blocks for a token window (surgery.py:550-551)."""
+    return -(-int(local_window) // int(route_block)) if local_window > 0 else 0
+
+
+def route_block_vote(assignments: torch.Tensor, r: int, route_block: int) -> torch.Tensor:
+    """(B, H, S, L, p) branch scores -> (B, H, ceil(S / route_block), r) int32 routing ids."""
+    if assignments.dim() != 5:
+        raise ValueError(f"assignments must be (B, H, S, levels, p); got {tuple(assignments.shape)}")
+    B, H, S, L, P = assignments.shape
+    r = int(r)
+    if not 0 <= r <= L:
+        raise ValueError(f"r={r} must lie in [0, {L}]")
+    if route_block < 1:
+        raise ValueError("route_block must be >= 1")
+    dev = nat.require_device(assignments)
+    a = assignments if assignments.dtype in _SCORE_DTYPES else assignments.float()
+    NB = -(-S // route_block)
+    out = torch.empty((B, H, NB, r), dtype=torch.int32, device=dev)
+    if out.numel() == 0:
+        return out
+    with torch.cuda.device(dev):
+        rc = nat.lib().sa_route_block_vote(nat.ptr(a), nat.dtype_code(a.dtype, _SCORE_DTYPES), nat.strides(a),
+                                           B, H, S, L, P, r, int(route_block), nat.ptr(out), nat.stream(dev))
+    nat.check(rc)
+    return out
+
+
+def block_list_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, assignments: torch.Tensor, r: int,
+                       *, p: int, route_block: int = 128, local_window: int = 16,
+                       sm_scale: Optional[float] = None, block_assignments: Optional[torch.Tensor] = None,
+                       return_stats: bool = False):
+    """Causal block-list prefill with block-granular tree routing.
+
+    q: (B, H, S, D); k, v: (B, H_kv, S, D). ``assignments``: (B, H, S, L, p)
+    per-token branch scores, or (B, H, NB, L, p) per-block scores when
+    NB != S (direct block routing); ``block_assignments`` of shape
+    (B, H, NB, L, p) take precedence, as in the reference. ``r``: routed
+    levels (req_depth). Returns the attention output, plus a dict with
+    ``mean_allowed_keys``, ``mean_causal_keys`` and ``block_density``
+    (surgery.py:589-595; host reads) when ``return_stats``.
+    """
+    B, H, S, _ = q.shape
+    RB = int(route_block)
+    NB = -(-S // RB)
+    if block_assignments is not None and block_assignments.shape[2] == NB:
+        route = route_block_vote(block_assignments[:, :, :NB], r, 1)
+    elif assignments.shape[2] == NB and NB != S:
+        route = route_block_vote(assignments[:, :, :NB], r, 1)
+    else:
+        route = route_block_vote(assignments[:, :, :S], r, RB)
+    bl = build_block_lists(route, r, is_causal=True, sink_block=True,
+                           local_blocks=local_blocks_of(local_window, RB), arity=p)
+    out = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True, sm_scale=sm_scale)
+    if not return_stats:
+        return out
+    lens = torch.full((NB,), RB, dtype=torch.float32, device=q.device)
+    lens[-1] = S - (NB - 1) * RB
+    c = bl.counts.to(torch.float32)
+    allowed = ((c - 1) * RB * lens + lens * (lens + 1) / 2).sum(-1)
+    stats = {
+        "mean_allowed_keys": (allowed.mean() / S).item(),
+        "mean_causal_keys": (S + 1) / 2,
+        "block_density": (c.sum() / (B * H * NB * (NB + 1) / 2)).item(),
+    }
+    return out, stats

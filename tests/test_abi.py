@@ -71,6 +71,20 @@ def test_host_side_argument_errors():
     assert lib.sa_decode_workspace_bytes(64, 32, 8, 128, 2048) == 0
 
 
+def test_route_vote_argument_errors():
+    lib = nat.lib()
+    p = ctypes.c_void_p(16)
+    st5 = (ctypes.c_int64 * 5)(1, 1, 1, 1, 1)
+    out = ctypes.c_void_p(16)
+    # r beyond the levels, zero route block, too many branches, bad dtype
+    assert lib.sa_route_block_vote(p, 0, st5, 1, 1, 8, 2, 2, 3, 4, out, None) == nat.SA_EINVAL
+    assert lib.sa_route_block_vote(p, 0, st5, 1, 1, 8, 2, 2, 1, 0, out, None) == nat.SA_EINVAL
+    assert lib.sa_route_block_vote(p, 0, st5, 1, 1, 8, 2, 65, 1, 4, out, None) == nat.SA_EUNSUPPORTED
+    assert lib.sa_route_block_vote(p, 3, st5, 1, 1, 8, 2, 2, 1, 4, out, None) == nat.SA_EINVAL
+    # empty problem: no launch, OK
+    assert lib.sa_route_block_vote(p, 0, st5, 0, 1, 8, 2, 2, 1, 4, out, None) == nat.SA_OK
+
+
 def test_python_layer_raises_on_cpu_tensors():
     from ultrametric import block_list_attention, build_block_lists, ultrametric_decode
     r = torch.zeros(1, 1, 4, 2, dtype=torch.int32)

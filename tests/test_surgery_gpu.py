@@ -1,0 +1,93 @@
+"""GPU parity of the surgery caller (src/llama_surgery/surgery.py:521-601):
+the HIP route-block vote bit-exact against the oracle (fp32 / bf16 / fp16
+scores, strided inputs, direct block routing, config-5 shape), and
+block_list_prefill against the masked-dense oracle on the reference test's
+grid (tests/test_surgery_block_list.py:61-95: fp16 <= 2e-3, statistics equal
+to the token-mask counts), plus GQA."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import blocks as ob
+from oracle import surgery as osg
+from ultrametric import block_list_prefill, route_block_vote
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("S,rb,r,p,L", [(200, 32, 2, 2, 4), (333, 16, 4, 4, 4), (1000, 128, 3, 5, 3),
+                                        (7, 128, 2, 2, 2)])
+def test_vote_matches_oracle(dtype, S, rb, r, p, L):
+    g = torch.Generator().manual_seed(S * p + r)
+    a = torch.randn(2, 3, S, L, p, generator=g).to(dtype)
+    ref = osg.majority_route(a.float().numpy(), r, rb)
+    got = route_block_vote(a.to(DEV), r, rb)
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def test_vote_ties_and_strided():
+    # quantised scores: many exact ties between branches and between vote counts
+    g = torch.Generator().manual_seed(3)
+    a = torch.randint(0, 2, (1, 4, 300, 2, 3), generator=g).float()
+    ref = osg.majority_route(a.numpy(), 2, 8)
+    assert np.array_equal(route_block_vote(a.to(DEV), 2, 8).cpu().numpy(), ref)
+    # non-contiguous view: levels and branches permuted in memory
+    base = torch.randn(1, 4, 300, 3, 2, generator=g)
+    view = base.transpose(-1, -2)            # (1, 4, 300, 2, 3), strided
+    ref = osg.majority_route(view.contiguous().numpy(), 2, 32)
+    assert np.array_equal(route_block_vote(view.to(DEV), 2, 32).cpu().numpy(), ref)
+    # direct block routing (route_block = 1)
+    ref = osg.direct_route(view.contiguous().numpy(), 2)
+    assert np.array_equal(route_block_vote(view.to(DEV), 2, 1).cpu().numpy(), ref)
+
+
+def test_vote_config5_shape():
+    # config 5: 32 heads, N = 16384, route block 128, p = 4, 4 levels, r = 2
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn(1, 32, 16384, 4, 4, generator=g)
+    ref = osg.majority_route(a.numpy(), 2, 128)
+    assert np.array_equal(route_block_vote(a.to(DEV), 2, 128).cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("S,rb,lw,r", [(200, 32, 16, 2), (256, 64, 0, 3), (96, 32, 40, 1)])
+def test_block_list_prefill_matches_oracle(S, rb, lw, r):
+    torch.manual_seed(S + r)
+    B, H, D, L, p = 1, 2, 32, 4, 2
+    q, k, v = (torch.randn(B, H, S, D).to(torch.float16) for _ in range(3))
+    assign = torch.softmax(torch.randn(B, H, S, L, p), dim=-1)
+    scale = 1.0 / math.sqrt(D)
+    out, st = block_list_prefill(q.to(DEV), k.to(DEV), v.to(DEV), assign.to(DEV), r, p=p, route_block=rb,
+                                 local_window=lw, sm_scale=scale, return_stats=True)
+    route = osg.majority_route(assign.numpy(), r, rb)
+    bl = ob.build_block_lists(route, r, is_causal=True, sink_block=True,
+                              local_blocks=osg.local_blocks_of(lw, rb), arity=p)
+    mask = ob.lists_to_mask(bl.lists, bl.counts)
+    ref, _ = oa.block_sparse_attention_ref(q.float().numpy(), k.float().numpy(), v.float().numpy(), mask, rb,
+                                           is_causal=True, sm_scale=scale)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-3
+    tm = oa.token_mask_from_blocks(mask, rb, S, is_causal=True)
+    assert abs(st["mean_allowed_keys"] - tm.sum(-1).mean()) < 1e-3
+    assert abs(st["mean_causal_keys"] - (S + 1) / 2) < 1e-9
+
+
+def test_block_list_prefill_gqa_bf16_direct_blocks():
+    torch.manual_seed(9)
+    B, H, Hkv, S, D, L, p, rb, r = 1, 8, 2, 640, 64, 3, 4, 128, 2
+    q = torch.randn(B, H, S, D).to(torch.bfloat16)
+    k, v = (torch.randn(B, Hkv, S, D).to(torch.bfloat16) for _ in range(2))
+    NB = S // rb
+    blk = torch.randn(B, H, NB, L, p)            # per-block scores: direct routing
+    out = block_list_prefill(q.to(DEV), k.to(DEV), v.to(DEV), blk.to(DEV), r, p=p, route_block=rb,
+                             local_window=16)
+    route = osg.direct_route(blk.numpy(), r)
+    bl = ob.build_block_lists(route, r, is_causal=True, sink_block=True, local_blocks=1, arity=p)
+    mask = ob.lists_to_mask(bl.lists, bl.counts)
+    ref, _ = oa.block_sparse_attention_ref(q.float().numpy(), k.float().numpy(), v.float().numpy(), mask, rb,
+                                           is_causal=True)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
