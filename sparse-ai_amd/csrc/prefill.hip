@@ -313,11 +313,16 @@ void prefill_mfma_kernel(FwdParams p) {
   // ---- LDS layout of a stage: K tile then V tile, BN rows of ROWB bytes,
   // 16-byte chunk c of row r stored at position c ^ f(r):
   //   K: f = (r >> RSH) & (CPR-1)  -> the 16 rows read by one MFMA operand
-  //      fetch hit 16 distinct bank groups;
-  //   V: f = 2 (r & 3) & (CPR-1)   -> the 4 rows x 32 bytes of one transpose
-  //      read (ds_read_b64_tr_b16) hit distinct bank groups.
+  //      fetch hit 16 distinct 16-byte bank groups;
+  //   V: f = 4 sigma(r) + 2 tau(r) -> XORs the 64-byte segment (sigma) and
+  //      32-byte half (tau) of a row, so that the 4 rows x 32 bytes of a
+  //      16-lane transpose read (ds_read_b64_tr_b16) and the 4 rows x 64
+  //      bytes of a 32-lane one land in distinct banks of a 128-byte and of
+  //      a 256-byte bank window alike.
   auto fk = [](int r) { return (r >> RSH) & (CPR - 1); };
-  auto fv = [](int r) { return (2 * (r & 3)) & (CPR - 1); };
+  auto vsig = [](int r) { return D == 128 ? (r & 3) : (D == 64 ? ((r >> 1) & 1) : 0); };
+  auto vtau = [](int r) { return D == 64 ? (r & 1) : ((r >> 1) & 1); };
+  auto fv = [&](int r) { return 4 * vsig(r) + 2 * vtau(r); };
 
   // Direct-to-LDS loads: load i of this wave fills 1-KB block `blk` of the
   // K (isk) or V tile: lane L writes slot 64 blk + L = (row, position), and
@@ -377,23 +382,35 @@ void prefill_mfma_kernel(FwdParams p) {
   // (g = lane / 16, j = lane % 16) lane j addresses row 4 kh + (j >> 2)
   // (+ 16 s2 + 8 for the second half) and columns 4 (j & 3) + 16 (g & 1) of
   // the 32-column tile dt; the hardware hands lane i the values of column
-  // i (+16 (g & 1)) of the four addressed rows.
-  uint32_t v_rd_even, v_rd_odd;
+  // i (+16 (g & 1)) of the four addressed rows. Rows r and r + 8 share the
+  // swizzle, so the row offsets stay immediates; one address per tile dt.
+  uint32_t v_rd[DT];
   {
     const int g = lane >> 4, j = lane & 15;
     const int vr = 4 * kh + (j >> 2);
-    const int clane = ((j & 3) >> 1) + 2 * (g & 1);
-    const int f = fv(vr);
-    const uint32_t b = TILEB + vr * ROWB + 16 * (clane ^ (f & 3)) + 8 * (j & 1);
-    const int flip = f >> 2;   // chunk bit 2 of the swizzle flips the dt parity
-    v_rd_even = b + 64 * flip;
-    v_rd_odd = b - 64 * flip;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      v_rd[dt] = TILEB + vr * ROWB + 64 * (dt ^ vsig(vr)) + 32 * ((g & 1) ^ vtau(vr)) + 16 * ((j & 3) >> 1) +
+                 8 * (j & 1);
+    }
   }
 
   f32x16_t acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16_t{};
   float m_i = -INFINITY, l_i = 0.f;
+
+  // The first S - 1 tiles come from the row's first list entries (the first
+  // two when a route block holds one tile), read with uniform loads at entry:
+  // their K / V loads are issued before the row's count and list have
+  // arrived. The row has max_count readable entries; issue() clamps any key
+  // out of range, so this is safe for short or empty rows too (loads that no
+  // tile consumes are drained before the kernel ends).
+  const int e0 = p.max_count > 0 ? list[0] : 0;
+  const int e1 = p.max_count > 1 ? list[1] : 0;
+  auto early_key = [&](int m) { return ((m >> lspb) == 0 ? e0 : e1) * p.RB + (m & (spb - 1)) * BN; };
+#pragma unroll
+  for (int st0 = 0; st0 < S - 1; ++st0) issue(early_key(st0), st0);
 
   // Folds tile n (first key key0, held in stage stg) into the running state.
   auto compute = [&](int n, int key0, int stg) {
@@ -455,11 +472,11 @@ void prefill_mfma_kernel(FwdParams p) {
     // (e < 4) or 16 s2 + 8 + 4 kh + (e - 4): the first / second transpose read.
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const uint32_t vb = (dt & 1) ? v_rd_odd : v_rd_even;
+      const uint32_t vb = v_rd[dt];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        SA_LDS s16x4_t* a0 = (SA_LDS s16x4_t*)((SA_LDS char*)sbase + vb + (16 * s2) * ROWB + 64 * dt);
-        SA_LDS s16x4_t* a1 = (SA_LDS s16x4_t*)((SA_LDS char*)sbase + vb + (16 * s2 + 8) * ROWB + 64 * dt);
+        SA_LDS s16x4_t* a0 = (SA_LDS s16x4_t*)((SA_LDS char*)sbase + vb + (16 * s2) * ROWB);
+        SA_LDS s16x4_t* a1 = (SA_LDS s16x4_t*)((SA_LDS char*)sbase + vb + (16 * s2 + 8) * ROWB);
         const u32x2_t lo = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(a0));
         const u32x2_t hi = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(a1));
         acc[dt] = Mma<T>::mma(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pb[s2], acc[dt]);
@@ -479,7 +496,8 @@ void prefill_mfma_kernel(FwdParams p) {
     }
     __syncthreads();
     // No compiler-visible load may be outstanding once the pipeline runs (the
-    // explicit vmcnt waits below count only the pipeline's own loads).
+    // explicit vmcnt waits below count only the pipeline's own loads; the
+    // early tiles of segment 0 are among them).
     __builtin_amdgcn_s_waitcnt(0);
     const int total = seg_n * spb;
     auto tile_key0 = [&](int m) { return list_lds[m >> lspb] * p.RB + (m & (spb - 1)) * BN; };
@@ -492,8 +510,12 @@ void prefill_mfma_kernel(FwdParams p) {
     int key_of[S];
 #pragma unroll
     for (int st0 = 0; st0 < S - 1; ++st0) {
-      key_of[st0] = st0 < total ? tile_key0(st0) : 0;
-      if (st0 < total) issue(key_of[st0], st0);
+      if (seg == 0) {
+        key_of[st0] = early_key(st0);   // already issued
+      } else {
+        key_of[st0] = st0 < total ? tile_key0(st0) : 0;
+        if (st0 < total) issue(key_of[st0], st0);
+      }
     }
     key_of[S - 1] = 0;
     int next_key = S - 1 < total ? tile_key0(S - 1) : 0;
@@ -520,6 +542,7 @@ void prefill_mfma_kernel(FwdParams p) {
     }
   }
 
+  wait_vmcnt<0>();   // early tiles of an empty or short row
   const float l_tot = l_i + __shfl_xor(l_i, 32);
   if (qpos < N) {
     const float inv = 1.f / (l_tot == 0.f ? 1.f : l_tot);
