@@ -59,6 +59,8 @@ def parse_args():
     ap.add_argument("--cpu-heads", type=int, default=32, help="heads timed for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU work for the CPU baseline (whole passes over --cpu-heads)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also run config 3: density sweep at N in {2048, 8192, 32768} against the dense case")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (reference for HBM byte counters)")
     return ap.parse_args()
@@ -91,6 +93,61 @@ def time_launches(fn, reps, torch):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / reps
+
+
+def density_sweep(torch, wl, nat, dev, reps):
+    """Config 3: bf16, H32, D128, causal, route block 128; per head Bernoulli(rho) over the
+    lower-triangular blocks + diagonal + sink, rho in {1, .5, .25, .0625, .016}, N in
+    {2048, 8192, 32768}. Each point times the prefill kernel over those lists (raw ABI,
+    HIP events); the dense case of the same build is rho = 1 (every causal block listed);
+    torch's scaled_dot_product_attention (causal) is timed as an external dense reference.
+    Returns one record per point: listed fraction of causal blocks, time, TFLOP/s on listed
+    tiles, speedup over the dense case of the same build and over SDPA."""
+    from ultrametric import block_lists_from_mask
+    import torch.nn.functional as F
+    out = []
+    Z, H, D, RB = 1, 32, 128, 128
+    for N in (2048, 8192, 32768):
+        NB = N // RB
+        g = torch.Generator(device=dev).manual_seed(3)
+        q, k, v = (torch.randn(Z, H, N, D, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+                   for _ in range(3))
+        o = torch.empty_like(q)
+        st = [nat.strides(t) for t in (q, k, v, o)]
+        stream = nat.stream(dev)
+        causal_blocks = Z * H * NB * (NB + 1) // 2
+        dense_ms = None
+        with torch.no_grad():
+            sdpa = lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True)  # noqa: E731
+            try:
+                sdpa_ms = time_launches(sdpa, reps, torch)
+            except RuntimeError:
+                sdpa_ms = None
+            for rho in (1.0, 0.5, 0.25, 0.0625, 0.016):
+                mask = wl.bernoulli_block_mask(Z, H, NB, rho, seed=3 + int(rho * 1e6)).to(dev)
+                bl = block_lists_from_mask(mask, is_causal=True)
+                lists = bl.lists.contiguous()
+                tiles = int(bl.counts.sum())
+
+                def fwd():
+                    nat.check(nat.lib().sa_block_sparse_fwd(
+                        nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(o), None, nat.ptr(lists), nat.ptr(bl.counts),
+                        None, 0, Z, H, H, N, D, RB, bl.max_count, st[0], st[1], st[2], st[3], None,
+                        1.0 / math.sqrt(D), 1, 1, stream))
+                ms = time_launches(fwd, reps, torch)
+                if rho == 1.0:
+                    dense_ms = ms
+                flop = 4.0 * D * RB * RB * tiles
+                out.append({"N": N, "rho": rho, "listed_fraction_causal": round(tiles / causal_blocks, 5),
+                            "ms": round(ms, 5), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                            "speedup_vs_dense_same_build": round(dense_ms / ms, 3),
+                            "speedup_vs_sdpa": None if sdpa_ms is None else round(sdpa_ms / ms, 3),
+                            "sdpa_ms": None if sdpa_ms is None else round(sdpa_ms, 5)})
+                log(f"sweep N={N} rho={rho}: {ms * 1e3:.1f} us, listed {tiles / causal_blocks:.4f} of causal blocks")
+                del mask, bl, lists
+        del q, k, v, o
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
@@ -221,6 +278,10 @@ def main():
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = src.numel() * src.element_size()
         del src, dst
+
+    # ---------------- config 3: density sweep (optional) ------------------------------
+    if args.sweep:
+        result["sweep"] = density_sweep(torch, wl, nat, dev, reps=max(20, args.steps // 4))
 
     # ---------------- config 4: sparse paged decode -----------------------------------
     if not args.no_decode:
