@@ -130,6 +130,40 @@ int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, 
                         int dtype, int is_causal, void* stream);
 
 /*
+ * Block-sparse attention backward over block lists.
+ * Replaces: _block_list_attention_bwd with _block_list_bwd_dq_kernel and
+ *   _block_list_bwd_dkdv_kernel (src/ultrametric/block_list.py:758-880,
+ *   :494-681), GQA added (dk / dv sum over the H / H_kv query heads of a kv
+ *   head).
+ *
+ * q, out, dout, dq  (Z, H, N, D); k, v, dk, dv (Z, H_kv, N, D); element type
+ *             dtype for all; strides *_strides[4].
+ * lse         (Z, H, N) fp32 contiguous: the forward's natural-log LSE.
+ * lists / counts / max_count: the forward's block lists.
+ * t_lists / t_counts / t_max_count: the transposed lists
+ *             (build_transposed_block_lists, block_list.py:281-327): per
+ *             (z, h, key block), the ascending query blocks that list it;
+ *             (Z, H, NB, t_max_count) / (Z, H, NB) int32 contiguous.
+ * soft_bias   optional (Z, H, NB, max_count) per-listed-block logit bias, as in
+ *             the forward; d_soft_bias (Z, H, NB, max_count) fp32 contiguous
+ *             receives its gradient (sum of dL/dlogit over the block pair) and
+ *             must be zero-filled by the caller (the kernel accumulates with
+ *             float atomics, so its low bits depend on the order of the adds).
+ * delta       (Z, H, N) fp32 contiguous workspace (rowsum(dout * out)).
+ * dq, dk, dv are fully written (zeros where no pair is visible).
+ */
+int sa_block_sparse_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                        const float* lse, const int32_t* lists, const int32_t* counts, int max_count,
+                        const int32_t* t_lists, const int32_t* t_counts, int t_max_count,
+                        const void* soft_bias, int soft_bias_dtype, const int64_t* sb_strides,
+                        float* delta, void* dq, void* dk, void* dv, float* d_soft_bias, int Z, int H,
+                        int H_kv, int N, int D, int route_block, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                        const int64_t* do_strides, const int64_t* dq_strides, const int64_t* dk_strides,
+                        const int64_t* dv_strides, float sm_scale, int dtype, int is_causal,
+                        void* stream);
+
+/*
  * Workspace bytes needed by sa_sparse_paged_decode for B sequences of H query
  * heads (H_kv kv heads) of dimension D with at most max_pages logical pages
  * each. 0 when B * H_kv work items already fill the GPU, so that each

@@ -111,6 +111,72 @@ def block_sparse_attention_ref(q: np.ndarray, k: np.ndarray, v: np.ndarray, bloc
     return out, lse
 
 
+def block_sparse_attention_grad_ref(q: np.ndarray, k: np.ndarray, v: np.ndarray, block_mask: np.ndarray,
+                                    route_block: int, dout: np.ndarray, *, is_causal: bool = False,
+                                    sm_scale: Optional[float] = None,
+                                    pair_bias: Optional[np.ndarray] = None):
+    """Gradients of ``block_sparse_attention_ref``'s output, float64
+    (the analytic backward of block_list.py:494-681,758-880):
+    with P = softmax(S) over the visible columns of a row,
+      dV += P^T dO, dS = P * (dO V^T - rowsum(dO * O)),
+      dQ += scale dS K, dK += scale dS^T Q,
+    and the gradient of the per-block-pair logit bias is the sum of dS over
+    the pair. k / v may carry H_kv | H heads (their gradients sum over the
+    query heads that read them).
+    Returns (dq, dk, dv, d_pair_bias (Z, H, NB, NB)) as float64.
+    """
+    Z, H, N, D = q.shape
+    Hkv = k.shape[1]
+    group = H // Hkv
+    NB = block_mask.shape[-1]
+    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(D)
+    dq = np.zeros((Z, H, N, D))
+    dk = np.zeros((Z, Hkv, N, D))
+    dv = np.zeros((Z, Hkv, N, D))
+    dpb = np.zeros((Z, H, NB, NB))
+    for z in range(Z):
+        for h in range(H):
+            kh = h // group
+            kf = k[z, kh].astype(np.float64)
+            vf = v[z, kh].astype(np.float64)
+            for qb in range(NB):
+                r0, r1 = qb * route_block, min(N, (qb + 1) * route_block)
+                if r0 >= N:
+                    break
+                kbs = np.nonzero(block_mask[z, h, qb])[0]
+                if kbs.size == 0:
+                    continue
+                cols = np.concatenate([np.arange(kb * route_block, min(N, (kb + 1) * route_block)) for kb in kbs])
+                cols = cols[cols < N]
+                if cols.size == 0:
+                    continue
+                rows = np.arange(r0, r1)
+                m = np.ones((rows.size, cols.size), dtype=bool)
+                if is_causal:
+                    m &= rows[:, None] >= cols[None, :]
+                qf = q[z, h, r0:r1].astype(np.float64)
+                s = qf @ kf[cols].T * scale
+                if pair_bias is not None:
+                    s = s + pair_bias[z, h, qb][cols // route_block][None, :].astype(np.float64)
+                s = np.where(m, s, -np.inf)
+                mx = s.max(-1, keepdims=True)
+                mx = np.where(np.isfinite(mx), mx, 0.0)
+                e = np.where(m, np.exp(s - mx), 0.0)
+                den = e.sum(-1, keepdims=True)
+                pm = np.where(den > 0, e / np.where(den > 0, den, 1.0), 0.0)
+                do = dout[z, h, r0:r1].astype(np.float64)
+                o = pm @ vf[cols]
+                dp = do @ vf[cols].T
+                ds = pm * (dp - (do * o).sum(-1, keepdims=True))
+                dq[z, h, r0:r1] += scale * ds @ kf[cols]
+                np.add.at(dk[z, kh], cols, scale * ds.T @ qf)
+                np.add.at(dv[z, kh], cols, pm.T @ do)
+                colb = cols // route_block
+                for kb in kbs:
+                    dpb[z, h, qb, kb] += ds[:, colb == kb].sum()
+    return dq, dk, dv, dpb
+
+
 def masked_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, token_mask: np.ndarray,
                      sm_scale: Optional[float] = None) -> Tuple[np.ndarray, np.ndarray]:
     """block_list.py:371-378 with an explicit (Z, H, N, N) token mask, float64."""

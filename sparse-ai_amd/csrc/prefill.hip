@@ -631,7 +631,9 @@ extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, 
                                    const int64_t* sb_strides, float sm_scale, int dtype,
                                    int is_causal, void* stream) {
   using namespace sa;
-  if (!q || !k || !v || !out || !lists || !counts) return fail(SA_EINVAL, "NULL tensor argument");
+  if (!q || !k || !v || !out || !counts || (!lists && max_count > 0)) {
+    return fail(SA_EINVAL, "NULL tensor argument");
+  }
   if (!q_strides || !k_strides || !v_strides || !o_strides) return fail(SA_EINVAL, "NULL strides");
   if (Z < 0 || H < 0 || N < 0 || H_kv <= 0 || (H > 0 && H % H_kv != 0)) {
     return fail(SA_EINVAL, "bad Z/H/H_kv/N");

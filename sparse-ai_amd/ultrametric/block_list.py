@@ -306,7 +306,8 @@ def block_list_attention(
     HIP kernels pick their own tiles, but given values must still divide
     route_block (block_list.py:738-739). Returns out, or (out, lse) with lse
     the natural-log LSE of the scaled scores, (Z, H, N) fp32, -inf for rows
-    with no visible key.
+    with no visible key. Differentiable in q, k, v and ``soft_block_bias``
+    (block_list.py:883-961): the backward recomputes P from the saved LSE.
     """
     if not HAS_TRITON:
         raise RuntimeError("block_list_attention requires the HIP backend (libsparseattn.so)")
@@ -340,23 +341,101 @@ def block_list_attention(
     if soft_block_bias is not None:
         nat.require_device(q, soft_block_bias)
 
+    lists = lists.to(torch.int32).contiguous()
+    counts = counts.to(torch.int32).contiguous()
+    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(D)
     needs_grad = torch.is_grad_enabled() and (
         q.requires_grad or k.requires_grad or v.requires_grad
         or (soft_block_bias is not None and soft_block_bias.requires_grad))
     if needs_grad:
-        raise RuntimeError("block_list_attention: the backward pass is not implemented in the HIP "
-                           "build yet; call it under torch.no_grad() or with inputs that do not "
-                           "require grad")
-
-    lists = lists.to(torch.int32).contiguous()
-    counts = counts.to(torch.int32).contiguous()
-    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(D)
+        return _BlockListAttentionFn.apply(q, k, v, soft_block_bias, lists, counts, int(max_count),
+                                           int(route_block), bool(is_causal), float(scale), bool(return_lse))
     out = torch.empty((Z, H, N, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((Z, H, N), dtype=torch.float32, device=q.device) if return_lse else None
     _launch_fwd(q, k, v, out, lse, lists, counts, max_count,
                 soft_block_bias.detach() if soft_block_bias is not None else None,
                 route_block, is_causal, scale)
     return (out, lse) if return_lse else out
+
+
+# ----------------------------------------------------------------------------
+# Backward
+# ----------------------------------------------------------------------------
+
+def _launch_bwd(dout, q, k, v, out, lse, lists, counts, max_count, soft_block_bias, route_block,
+                is_causal, scale):
+    """dq, dk, dv (and the soft-bias gradient) of block-list attention
+    (block_list.py:758-880): delta = rowsum(dout * out), dQ over the forward
+    lists, dK / dV over the transposed lists."""
+    Z, H, N, D = q.shape
+    Hkv = k.shape[1]
+    dev = q.device
+    nb = -(-N // route_block)
+    dt = nat.dtype_code(q.dtype, (torch.float32, torch.bfloat16, torch.float16))
+    if dout.dtype != q.dtype:
+        dout = dout.to(q.dtype)
+    t_lists, t_counts, t_max = build_transposed_block_lists(BlockLists(lists, counts, max_count),
+                                                            num_key_blocks=nb)
+    t_lists = t_lists.to(torch.int32).contiguous()
+    t_counts = t_counts.to(torch.int32).contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    delta = torch.empty((Z, H, N), dtype=torch.float32, device=dev)
+    sb = soft_block_bias
+    sb_code = 0
+    dsb = None
+    if sb is not None:
+        if sb.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            sb = sb.float()
+        sb_code = nat.DTYPE_CODES[sb.dtype]
+        dsb = torch.zeros((Z, H, nb, max_count), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = nat.lib().sa_block_sparse_bwd(
+            nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), nat.ptr(dout), nat.ptr(lse),
+            nat.ptr(lists) if max_count > 0 else None, nat.ptr(counts), int(max_count),
+            nat.ptr(t_lists) if t_max > 0 else None, nat.ptr(t_counts), int(t_max),
+            nat.ptr(sb), sb_code, nat.strides(sb) if sb is not None else None,
+            nat.ptr(delta), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dsb),
+            Z, H, Hkv, N, D, int(route_block),
+            nat.strides(q), nat.strides(k), nat.strides(v), nat.strides(out), nat.strides(dout),
+            nat.strides(dq), nat.strides(dk), nat.strides(dv), float(scale), dt, int(bool(is_causal)),
+            nat.stream(dev))
+    nat.check(rc)
+    return dq, dk, dv, dsb
+
+
+class _BlockListAttentionFn(torch.autograd.Function):
+    """Autograd wrapper of the HIP forward / backward (block_list.py:883-961)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, soft_block_bias, lists, counts, max_count, route_block, is_causal, scale,
+                return_lse):
+        Z, H, N, D = q.shape
+        out = torch.empty((Z, H, N, D), dtype=q.dtype, device=q.device)
+        lse = torch.empty((Z, H, N), dtype=torch.float32, device=q.device)
+        sb = soft_block_bias.detach() if soft_block_bias is not None else None
+        _launch_fwd(q, k, v, out, lse, lists, counts, max_count, sb, route_block, is_causal, scale)
+        ctx.save_for_backward(q, k, v, out, lse, lists, counts, sb)
+        ctx.max_count, ctx.route_block, ctx.is_causal, ctx.scale = max_count, route_block, is_causal, scale
+        ctx.sb_dtype = soft_block_bias.dtype if soft_block_bias is not None else None
+        if return_lse:
+            ctx.mark_non_differentiable(lse)
+            return out, lse
+        return out
+
+    @staticmethod
+    def backward(ctx, dout, *unused):
+        q, k, v, out, lse, lists, counts, sb = ctx.saved_tensors
+        dq, dk, dv, dsb = _launch_bwd(dout, q, k, v, out, lse, lists, counts, ctx.max_count, sb,
+                                      ctx.route_block, ctx.is_causal, ctx.scale)
+        if dsb is not None and ctx.sb_dtype is not None:
+            dsb = dsb.to(ctx.sb_dtype)
+        return (dq if ctx.needs_input_grad[0] else None,
+                dk if ctx.needs_input_grad[1] else None,
+                dv if ctx.needs_input_grad[2] else None,
+                dsb if ctx.needs_input_grad[3] else None,
+                None, None, None, None, None, None, None)
 
 
 def routed_block_attention(

@@ -20,9 +20,11 @@ block-list kernel in the reference, as free functions over the same inputs
   ``repeat_kv`` (surgery.py:77-86). Optional statistics follow
   surgery.py:589-595.
 
-The reference's straight-through soft-bias gradient (surgery.py:566-588)
-needs the block-list backward, which this build does not provide: a call
-that requires gradients raises RuntimeError (as block_list_attention does).
+Gradients with respect to q, k and v flow through block_list_attention's
+backward. The router's straight-through soft-bias term (surgery.py:566-588)
+is built from the model's expected block distances; a caller that has them
+passes the resulting bias to block_list_attention (``soft_block_bias``), whose
+backward returns its gradient.
 """
 
 from __future__ import annotations
