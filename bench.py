@@ -333,6 +333,33 @@ def main():
                          "traffic_source": "profiles/decode_config4_bf16.md"},
         }
         log(f"decode {dec_ms * 1e3:.1f} us/call, {dec_gbs:.0f} GB/s on routed bytes")
+
+        # same decode with packed routing codes: 4 bytes per (page, head) instead of 4 * TD
+        from ultrametric.kernel_decode import pack_routing_codes
+        bpl = max(1, int(max(w.router.max().item(), w.q_router.max().item())).bit_length())
+        pc, qc = pack_routing_codes(w.router, bpl), pack_routing_codes(w.q_router, bpl)
+        pout = torch.empty_like(w.q)
+        pargs = list(dargs)
+        pargs[5], pargs[6], pargs[7] = nat.ptr(pc), nat.ptr(qc), nat.ptr(pout)
+        pargs[23], pargs[24] = nat.strides(pc), nat.strides(qc)
+        pargs.insert(14, bpl)
+        pdec_fn = nat.lib().sa_sparse_paged_decode_codes
+
+        def pdec():
+            nat.check(pdec_fn(*pargs))
+
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                pdec()
+            pdec_ms = time_launches(pdec, max(50, args.steps), torch)
+        assert torch.equal(pout, dout), "packed-code decode disagrees with the int32-level decode"
+        pgbs = b_alg / (pdec_ms * 1e-3) / 1e9
+        result["decode"]["packed_codes"] = {
+            "bits_per_level": bpl, "ms_per_call": round(pdec_ms, 5), "gbs_routed": round(pgbs, 1),
+            "routing_metadata_bytes": int(w.context_lens.add(15).div(16, rounding_mode="floor").sum()) * (4 + 32 * 4),
+            "frac": round(pgbs / PEAK_HBM_GBS, 4),
+        }
+        log(f"decode (packed codes) {pdec_ms * 1e3:.1f} us/call, {pgbs:.0f} GB/s on routed bytes")
         del w
 
     # ---------------- CPU baseline (oracle, host cores) --------------------------------

@@ -206,6 +206,46 @@ int sa_sparse_paged_decode(const void* q, const void* k_cache, const void* v_cac
                            int dtype, void* stream);
 
 /*
+ * Packs routing levels into one 32-bit code per (row, head).
+ * Extension of ultrametric_decode (src/ultrametric/kernel_decode.py:22-124,
+ *   whose kernel re-reads TD int32 levels per (page, head), :76-81): the
+ *   packed per-page routing code that the hot-path scope lists as the next
+ *   step for decode. No reference counterpart.
+ *
+ * router      (rows, H, TD) int32, strides[3]; every level must lie in
+ *             [0, 2^bits_per_level).
+ * codes       (rows, H) uint32 contiguous output: level l is stored in bits
+ *             [bits_per_level (TD-1-l), bits_per_level (TD-l)), so level 0 is
+ *             the most significant field and the first r levels of two rows
+ *             agree iff their codes agree on the top bits_per_level * r bits.
+ * Limits: 1 <= bits_per_level <= 16, TD * bits_per_level <= 32.
+ */
+int sa_pack_page_codes(const int32_t* router, const int64_t* strides, int rows, int H, int TD,
+                       int bits_per_level, uint32_t* codes, void* stream);
+
+/*
+ * Sparse paged decode selecting pages by packed routing codes.
+ * Same computation as sa_sparse_paged_decode (kernel_decode.py:22-124 and
+ *   :188-247) with router / q_router replaced by their packed codes
+ *   (sa_pack_page_codes of the same levels): page_codes (P, H) uint32,
+ *   strides pc_strides[2]; q_codes (B, H) uint32, strides qc_strides[2].
+ *   Reads 4 bytes per (page, head) instead of 4 * TD. Results equal
+ *   sa_sparse_paged_decode's for levels that fit bits_per_level bits.
+ * Limits: as sa_pack_page_codes for TD and bits_per_level.
+ */
+int sa_sparse_paged_decode_codes(const void* q, const void* k_cache, const void* v_cache,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 const uint32_t* page_codes, const uint32_t* q_codes, void* out,
+                                 int B, int H, int H_kv, int D, int page_size, int TD,
+                                 int bits_per_level, int max_pages, int num_phys_pages,
+                                 int req_depth, int local_blocks, int sink_block,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* v_strides, const int64_t* bt_strides,
+                                 const int64_t* pc_strides, const int64_t* qc_strides,
+                                 const int64_t* o_strides, void* workspace, size_t workspace_bytes,
+                                 int dtype, void* stream);
+
+/*
  * Route-block majority vote of the surgery caller.
  * Replaces: the per-level majority vote of token argmax branches in
  *   SurgicalLlamaAttention._block_list_prefill

@@ -129,3 +129,31 @@ def dense_paged_loop(q, k_cache, v_cache, block_tables, context_lens):
             tot = sum(w)
             out[b][h] = [sum(wi * float(r[d]) for wi, r in zip(w, rows)) / tot for d in range(D)]
     return np.array(out)
+
+
+def pack_codes(router, bits_per_level):
+    """Packed routing code per (row, head): level l in bits [bpl*(TD-1-l), bpl*(TD-l)).
+
+    No reference counterpart (the reference decode compares int32 levels one by
+    one, kernel_decode.py:76-81); this states the packing that the packed decode
+    entry point consumes. Pinned by brute force (tests/test_oracle_decode.py):
+    for every depth r, the top bpl*r bits of two codes agree iff the first r
+    levels agree, and unpacking recovers every level.
+    """
+    router = np.asarray(router, dtype=np.int64)
+    td = router.shape[-1]
+    assert 1 <= bits_per_level <= 16 and td * bits_per_level <= 32
+    assert (router >= 0).all() and (router < (1 << bits_per_level)).all()
+    code = np.zeros(router.shape[:-1], dtype=np.uint64)
+    for lev in range(td):
+        code = (code << np.uint64(bits_per_level)) | router[..., lev].astype(np.uint64)
+    return code.astype(np.uint32)
+
+
+def prefix_mask(tree_depth, bits_per_level, req_depth):
+    """uint32 mask of the top bits_per_level * r bits, r = clamp(req_depth, 0, TD)."""
+    r = min(max(int(req_depth), 0), tree_depth)
+    if r == 0:
+        return np.uint32(0)
+    shift = bits_per_level * (tree_depth - r)
+    return np.uint32((0xFFFFFFFF << shift) & 0xFFFFFFFF)

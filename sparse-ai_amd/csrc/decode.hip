@@ -56,6 +56,10 @@ struct DecParams {
   float* part;
   int B, H, Hkv, D, PS, TD, max_pages, P, r, local, sink, G, splits;
   int vec_router;  // router rows allow one 16-byte load of 4 levels per (page, head)
+  const uint32_t* codes;    // packed mode: (P, H) page routing codes, or NULL
+  const uint32_t* qcodes;   // packed mode: (B, H) query routing codes
+  int64_t cs0, cs1, qcs0, qcs1;
+  uint32_t code_mask;       // bits of the first r levels (0 when r == 0)
   int64_t qs0, qs1, qs2;
   int64_t ks0, ks1, ks2;
   int64_t vs0, vs1, vs2;
@@ -210,10 +214,13 @@ void decode_kernel(DecParams p) {
     m_s[g] = -INFINITY;
     l_s[g] = 0.f;
   }
-  for (int i = tid; i < G * p.r; i += kDecThreads) {
-    const int g = i / p.r, lev = i % p.r;
-    qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
+  if (!p.codes) {
+    for (int i = tid; i < G * p.r; i += kDecThreads) {
+      const int g = i / p.r, lev = i % p.r;
+      qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
+    }
   }
+  const uint32_t qcode = p.codes ? p.qcodes[b * p.qcs0 + (h0 + gl) * p.qcs1] : 0u;
   __syncthreads();
   int qmine[4];                 // this lane's head's first four query levels (vector path)
 #pragma unroll
@@ -238,7 +245,19 @@ void decode_kernel(DecParams p) {
       }
     }
     bool hit[kPasses];
-    if (p.vec_router) {
+    if (p.codes) {
+      // Packed codes: one 32-bit word per (page, head); the first r levels
+      // agree iff the code bits under code_mask agree.
+      uint32_t cv[kPasses];
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
+        const bool need = !use_pre || ps * kPagesPerPass + pslot < r1;
+        cv[ps] = need ? p.codes[ph * p.cs0 + (h0 + gl) * p.cs1] : ~qcode;
+      }
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) hit[ps] = ((cv[ps] ^ qcode) & p.code_mask) == 0u;
+    } else if (p.vec_router) {
       int4 rv[kPasses];
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
@@ -533,17 +552,19 @@ extern "C" size_t sa_decode_workspace_bytes(int B, int H, int H_kv, int D, int m
   return static_cast<size_t>(B) * H * splits * (D + 2) * sizeof(float);
 }
 
-extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const void* v_cache,
-                                      const int32_t* block_tables, const int32_t* context_lens,
-                                      const int32_t* router, const int32_t* q_router, void* out,
-                                      int B, int H, int H_kv, int D, int page_size, int TD,
-                                      int max_pages, int num_phys_pages, int req_depth,
-                                      int local_blocks, int sink_block, const int64_t* q_strides,
-                                      const int64_t* k_strides, const int64_t* v_strides,
-                                      const int64_t* bt_strides, const int64_t* r_strides,
-                                      const int64_t* qr_strides, const int64_t* o_strides,
-                                      void* workspace, size_t workspace_bytes, int dtype,
-                                      void* stream) {
+namespace sa {
+namespace {
+
+// Shared by the two decode entry points: router / q_router (int32 levels) or
+// codes / qcodes (packed words, bpl bits per level, level 0 highest).
+int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                const int32_t* context_lens, const int32_t* router, const int32_t* q_router,
+                const uint32_t* codes, const uint32_t* qcodes, int bpl, void* out, int B, int H, int H_kv,
+                int D, int page_size, int TD, int max_pages, int num_phys_pages, int req_depth,
+                int local_blocks, int sink_block, const int64_t* q_strides, const int64_t* k_strides,
+                const int64_t* v_strides, const int64_t* bt_strides, const int64_t* r_strides,
+                const int64_t* qr_strides, const int64_t* o_strides, void* workspace,
+                size_t workspace_bytes, int dtype, void* stream) {
   using namespace sa;
   if (B < 0 || H < 0 || H_kv <= 0 || (H > 0 && H % H_kv != 0)) return fail(SA_EINVAL, "bad B/H/H_kv");
   const int G = H > 0 ? H / H_kv : 1;
@@ -561,7 +582,8 @@ extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const 
   }
   if (max_pages < 0 || num_phys_pages < 0) return fail(SA_EINVAL, "negative page counts");
   if (static_cast<long long>(B) * H == 0) return SA_OK;
-  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !router || !q_router || !out) {
+  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out ||
+      (codes ? (!qcodes) : (!router || !q_router))) {
     return fail(SA_EINVAL, "NULL tensor argument");
   }
   if (!q_strides || !k_strides || !v_strides || !bt_strides || !r_strides || !qr_strides || !o_strides) {
@@ -597,18 +619,103 @@ extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const 
   p.r = req_depth < 0 ? 0 : (req_depth > TD ? TD : req_depth);
   p.local = local_blocks; p.sink = sink_block != 0; p.G = G;
   p.splits = splits_for(B, H_kv, max_pages);
-  p.vec_router = r_strides[2] == 1 && TD >= 4 && p.r <= 4 && r_strides[0] % 4 == 0 &&
-                 r_strides[1] % 4 == 0 && (reinterpret_cast<uintptr_t>(router) & 15) == 0;
+  if (codes) {
+    p.codes = codes;
+    p.qcodes = qcodes;
+    p.cs0 = r_strides[0]; p.cs1 = r_strides[1];
+    p.qcs0 = qr_strides[0]; p.qcs1 = qr_strides[1];
+    const int shift = bpl * (TD - p.r);
+    p.code_mask = p.r == 0 ? 0u : (shift >= 32 ? 0u : (0xFFFFFFFFu << shift));
+  } else {
+    p.vec_router = r_strides[2] == 1 && TD >= 4 && p.r <= 4 && r_strides[0] % 4 == 0 &&
+                   r_strides[1] % 4 == 0 && (reinterpret_cast<uintptr_t>(router) & 15) == 0;
+  }
   p.qs0 = q_strides[0]; p.qs1 = q_strides[1]; p.qs2 = q_strides[2];
   p.ks0 = k_strides[0]; p.ks1 = k_strides[1]; p.ks2 = k_strides[2];
   p.vs0 = v_strides[0]; p.vs1 = v_strides[1]; p.vs2 = v_strides[2];
   p.bts0 = bt_strides[0]; p.bts1 = bt_strides[1];
-  p.rs0 = r_strides[0]; p.rs1 = r_strides[1]; p.rs2 = r_strides[2];
-  p.qrs0 = qr_strides[0]; p.qrs1 = qr_strides[1]; p.qrs2 = qr_strides[2];
+  if (!codes) {
+    p.rs0 = r_strides[0]; p.rs1 = r_strides[1]; p.rs2 = r_strides[2];
+    p.qrs0 = qr_strides[0]; p.qrs1 = qr_strides[1]; p.qrs2 = qr_strides[2];
+  }
   p.os0 = o_strides[0]; p.os1 = o_strides[1]; p.os2 = o_strides[2];
   p.qk_scale = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
   hipStream_t s = as_stream(stream);
   if (dtype == SA_DTYPE_F32) return launch_decode<float>(p, s);
   if (dtype == SA_DTYPE_BF16) return launch_decode<bf16_t>(p, s);
   return launch_decode<f16_t>(p, s);
+}
+
+// Packs (rows, H, TD) int32 routing levels into one word per (row, head):
+// level l occupies bits [bpl (TD-1-l), bpl (TD-l)), so level 0 is highest and
+// a prefix of r levels is the top bpl r bits.
+__global__ __launch_bounds__(256) void pack_codes_kernel(const int32_t* r, int64_t s0, int64_t s1, int64_t s2,
+                                                          int rows, int H, int TD, int bpl, uint32_t* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(rows) * H) return;
+  const int row = static_cast<int>(i / H), h = static_cast<int>(i % H);
+  const uint32_t m = bpl >= 32 ? 0xFFFFFFFFu : ((1u << bpl) - 1u);
+  uint32_t c = 0;
+  for (int l = 0; l < TD; ++l) c = (c << bpl) | (static_cast<uint32_t>(r[row * s0 + h * s1 + l * s2]) & m);
+  out[i] = c;
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+                                      const int32_t* block_tables, const int32_t* context_lens,
+                                      const int32_t* router, const int32_t* q_router, void* out,
+                                      int B, int H, int H_kv, int D, int page_size, int TD,
+                                      int max_pages, int num_phys_pages, int req_depth,
+                                      int local_blocks, int sink_block, const int64_t* q_strides,
+                                      const int64_t* k_strides, const int64_t* v_strides,
+                                      const int64_t* bt_strides, const int64_t* r_strides,
+                                      const int64_t* qr_strides, const int64_t* o_strides,
+                                      void* workspace, size_t workspace_bytes, int dtype,
+                                      void* stream) {
+  return sa::decode_impl(q, k_cache, v_cache, block_tables, context_lens, router, q_router, nullptr, nullptr, 0,
+                         out, B, H, H_kv, D, page_size, TD, max_pages, num_phys_pages, req_depth, local_blocks,
+                         sink_block, q_strides, k_strides, v_strides, bt_strides, r_strides, qr_strides,
+                         o_strides, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int sa_sparse_paged_decode_codes(const void* q, const void* k_cache, const void* v_cache,
+                                            const int32_t* block_tables, const int32_t* context_lens,
+                                            const uint32_t* page_codes, const uint32_t* q_codes, void* out,
+                                            int B, int H, int H_kv, int D, int page_size, int TD,
+                                            int bits_per_level, int max_pages, int num_phys_pages,
+                                            int req_depth, int local_blocks, int sink_block,
+                                            const int64_t* q_strides, const int64_t* k_strides,
+                                            const int64_t* v_strides, const int64_t* bt_strides,
+                                            const int64_t* pc_strides, const int64_t* qc_strides,
+                                            const int64_t* o_strides, void* workspace,
+                                            size_t workspace_bytes, int dtype, void* stream) {
+  using namespace sa;
+  if (bits_per_level < 1 || bits_per_level > 16) return fail(SA_EINVAL, "bits_per_level must lie in [1, 16]");
+  if (TD < 1 || static_cast<long long>(TD) * bits_per_level > 32) {
+    return fail(SA_EINVAL, "tree depth x bits_per_level must be in [1, 32]");
+  }
+  if (!pc_strides || !qc_strides) return fail(SA_EINVAL, "NULL strides");
+  return decode_impl(q, k_cache, v_cache, block_tables, context_lens, nullptr, nullptr, page_codes, q_codes,
+                     bits_per_level, out, B, H, H_kv, D, page_size, TD, max_pages, num_phys_pages, req_depth,
+                     local_blocks, sink_block, q_strides, k_strides, v_strides, bt_strides, pc_strides,
+                     qc_strides, o_strides, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int sa_pack_page_codes(const int32_t* router, const int64_t* strides, int rows, int H, int TD,
+                                  int bits_per_level, uint32_t* codes, void* stream) {
+  using namespace sa;
+  if (rows < 0 || H < 0 || TD < 1) return fail(SA_EINVAL, "bad rows/H/TD");
+  if (bits_per_level < 1 || bits_per_level > 16 || static_cast<long long>(TD) * bits_per_level > 32) {
+    return fail(SA_EINVAL, "need 1 <= bits_per_level <= 16 and tree depth x bits_per_level <= 32");
+  }
+  const long long n = static_cast<long long>(rows) * H;
+  if (n == 0) return SA_OK;
+  if (!router || !strides || !codes) return fail(SA_EINVAL, "NULL argument");
+  const long long g = (n + 255) / 256;
+  if (g > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
+  hipLaunchKernelGGL(pack_codes_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, as_stream(stream), router,
+                     strides[0], strides[1], strides[2], rows, H, TD, bits_per_level, codes);
+  return check_launch("page-code packing kernel");
 }

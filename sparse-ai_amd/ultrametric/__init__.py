@@ -20,7 +20,7 @@ from .block_list import (
     routed_block_attention,
 )
 from .kernel import block_sparse_attention, routing_to_block_indices
-from .kernel_decode import ultrametric_decode
+from .kernel_decode import pack_routing_codes, ultrametric_decode, ultrametric_decode_packed
 from .surgery import block_list_prefill, route_block_vote
 
 __all__ = [
@@ -35,6 +35,8 @@ __all__ = [
     "block_sparse_attention",
     "routing_to_block_indices",
     "ultrametric_decode",
+    "pack_routing_codes",
+    "ultrametric_decode_packed",
     "route_block_vote",
     "block_list_prefill",
 ]

@@ -21,7 +21,8 @@ from . import _native as nat
 
 HAS_TRITON = nat.available()
 
-__all__ = ["HAS_TRITON", "ultrametric_decode", "_ultrametric_decode_reference", "decode_workspace_bytes"]
+__all__ = ["HAS_TRITON", "ultrametric_decode", "_ultrametric_decode_reference", "decode_workspace_bytes",
+           "pack_routing_codes", "ultrametric_decode_packed"]
 
 
 def decode_workspace_bytes(batch_size: int, num_heads: int, head_dim: int, max_pages: int,
@@ -54,9 +55,59 @@ def ultrametric_decode(
     ``workspace`` (optional, uint8, >= decode_workspace_bytes(...)) avoids a
     per-call allocation. Returns (B, H, D) in q.dtype.
     """
-    batch_size, num_heads, head_dim = q.shape
     tree_depth = int(q_router_indices.shape[-1])
     assert tree_depth >= 1, "tree_depth must be >= 1"
+    rt = router_indices if router_indices.dtype == torch.int32 else router_indices.to(torch.int32)
+    qrt = q_router_indices if q_router_indices.dtype == torch.int32 else q_router_indices.to(torch.int32)
+    return _decode(q, k_cache, v_cache, block_tables, context_lens, rt, qrt, tree_depth, 0, req_depth,
+                   local_blocks, sink_block, workspace)
+
+
+def pack_routing_codes(router_indices: torch.Tensor, bits_per_level: int) -> torch.Tensor:
+    """Pack (rows, H, TD) routing levels into one 32-bit code per (row, head).
+
+    Level l lands in bits [bpl*(TD-1-l), bpl*(TD-l)) (level 0 most significant),
+    so a depth-r prefix match of two rows is equality of their top bpl*r bits.
+    Every level must lie in [0, 2**bits_per_level); TD * bits_per_level <= 32.
+    Returns a (rows, H) int32 tensor holding the uint32 bit patterns. Used once
+    per page write (the router of a page does not change), then passed to
+    ``ultrametric_decode_packed`` on every step.
+    """
+    if router_indices.dim() != 3:
+        raise ValueError(f"router_indices must be (rows, H, TD); got {tuple(router_indices.shape)}")
+    dev = nat.require_device(router_indices)
+    rows, H, TD = router_indices.shape
+    rt = router_indices if router_indices.dtype == torch.int32 else router_indices.to(torch.int32)
+    out = torch.empty((rows, H), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        rc = nat.lib().sa_pack_page_codes(nat.ptr(rt), nat.strides(rt), rows, H, TD, int(bits_per_level),
+                                          nat.ptr(out), nat.stream(dev))
+    nat.check(rc)
+    return out
+
+
+def ultrametric_decode_packed(q, k_cache, v_cache, block_tables, context_lens, page_codes, q_codes,
+                              tree_depth: int, bits_per_level: int, req_depth, local_blocks: int = 0,
+                              sink_block: bool = False, workspace: torch.Tensor = None):
+    """``ultrametric_decode`` with the routing vectors given as packed codes.
+
+    page_codes: (num_pages, H) and q_codes: (B, H), int32 tensors from
+    ``pack_routing_codes(router, bits_per_level)`` of a router with
+    ``tree_depth`` levels. Reads one 32-bit word per (page, head) where the
+    unpacked form reads tree_depth of them; the output is the same.
+    """
+    if page_codes.dim() != 2 or q_codes.dim() != 2:
+        raise ValueError("page_codes must be (num_pages, H) and q_codes (B, H)")
+    if page_codes.dtype != torch.int32 or q_codes.dtype != torch.int32:
+        raise ValueError("page_codes / q_codes must be int32 (as pack_routing_codes returns)")
+    return _decode(q, k_cache, v_cache, block_tables, context_lens, page_codes, q_codes, int(tree_depth),
+                   int(bits_per_level), req_depth, local_blocks, sink_block, workspace)
+
+
+def _decode(q, k_cache, v_cache, block_tables, context_lens, rt, qrt, tree_depth, bpl, req_depth,
+            local_blocks, sink_block, workspace):
+    """Shared validation and launch; bpl == 0 selects the int32-level router form."""
+    batch_size, num_heads, head_dim = q.shape
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         raise ValueError(f"k_cache / v_cache must be (pages, H_kv, page, D); got {tuple(k_cache.shape)}, "
                          f"{tuple(v_cache.shape)}")
@@ -64,16 +115,13 @@ def ultrametric_decode(
         raise ValueError("k_cache head_dim / head count incompatible with q")
     if not (q.dtype == k_cache.dtype == v_cache.dtype):
         raise ValueError("q, k_cache, v_cache must share dtype")
-    dev = nat.require_device(q, k_cache, v_cache, block_tables, context_lens, router_indices,
-                             q_router_indices)
+    dev = nat.require_device(q, k_cache, v_cache, block_tables, context_lens, rt, qrt)
     if k_cache.stride(3) != 1:
         k_cache = k_cache.contiguous()
     if v_cache.stride(3) != 1:
         v_cache = v_cache.contiguous()
     bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
     ctx = context_lens.to(torch.int32).contiguous()
-    rt = router_indices if router_indices.dtype == torch.int32 else router_indices.to(torch.int32)
-    qrt = q_router_indices if q_router_indices.dtype == torch.int32 else q_router_indices.to(torch.int32)
     num_pages, H_kv, page_size, _ = k_cache.shape
     max_pages = bt.shape[1]
     out = torch.empty((batch_size, num_heads, head_dim), dtype=q.dtype, device=dev)
@@ -84,15 +132,18 @@ def ultrametric_decode(
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     dt = nat.dtype_code(q.dtype, (torch.float32, torch.bfloat16, torch.float16))
     lib = nat.lib()
-    with torch.cuda.device(dev):
-        rc = lib.sa_sparse_paged_decode(
-            nat.ptr(q), nat.ptr(k_cache), nat.ptr(v_cache), nat.ptr(bt), nat.ptr(ctx), nat.ptr(rt),
-            nat.ptr(qrt), nat.ptr(out), batch_size, num_heads, H_kv, head_dim, page_size, tree_depth,
-            max_pages, num_pages, int(req_depth), int(local_blocks), int(bool(sink_block)),
+    head = (nat.ptr(q), nat.ptr(k_cache), nat.ptr(v_cache), nat.ptr(bt), nat.ptr(ctx), nat.ptr(rt),
+            nat.ptr(qrt), nat.ptr(out), batch_size, num_heads, H_kv, head_dim, page_size, tree_depth)
+    tail = (max_pages, num_pages, int(req_depth), int(local_blocks), int(bool(sink_block)),
             nat.strides(q), nat.strides(k_cache), nat.strides(v_cache), nat.strides(bt),
             nat.strides(rt), nat.strides(qrt), nat.strides(out),
             None if workspace is None else nat.ptr(workspace), 0 if workspace is None else workspace.numel(),
             dt, nat.stream(dev))
+    with torch.cuda.device(dev):
+        if bpl:
+            rc = lib.sa_sparse_paged_decode_codes(*head, bpl, *tail)
+        else:
+            rc = lib.sa_sparse_paged_decode(*head, *tail)
     nat.check(rc)
     return out
 

@@ -85,6 +85,22 @@ def test_route_vote_argument_errors():
     assert lib.sa_route_block_vote(p, 0, st5, 0, 1, 8, 2, 2, 1, 4, out, None) == nat.SA_OK
 
 
+
+def test_packed_code_argument_errors():
+    lib = nat.lib()
+    p = ctypes.c_void_p(16)
+    st3 = (ctypes.c_int64 * 3)(8, 4, 1)
+    # bits per level out of [1, 16]; TD * bits beyond 32; empty problem is OK
+    assert lib.sa_pack_page_codes(p, st3, 4, 2, 4, 0, p, None) == nat.SA_EINVAL
+    assert lib.sa_pack_page_codes(p, st3, 4, 2, 4, 17, p, None) == nat.SA_EINVAL
+    assert lib.sa_pack_page_codes(p, st3, 4, 2, 9, 4, p, None) == nat.SA_EINVAL
+    assert lib.sa_pack_page_codes(p, st3, 0, 2, 4, 4, p, None) == nat.SA_OK
+    st = [(ctypes.c_int64 * 4)(1, 1, 1, 1) for _ in range(7)]
+    args = [p] * 8 + [1, 4, 4, 64, 16, 4]
+    tail = [8, 8, 2, 0, 0] + st + [None, 0, 1, None]
+    assert lib.sa_sparse_paged_decode_codes(*args, 0, *tail) == nat.SA_EINVAL
+    assert lib.sa_sparse_paged_decode_codes(*args, 9, *tail) == nat.SA_EINVAL
+
 def test_python_layer_raises_on_cpu_tensors():
     from ultrametric import block_list_attention, build_block_lists, ultrametric_decode
     r = torch.zeros(1, 1, 4, 2, dtype=torch.int32)

@@ -109,3 +109,36 @@ def test_routed_bytes_counts_group_union_once():
     # req_depth 0: every page of every sequence, once per kv head
     assert pages == 2 * sum(-(-int(c) // 4) for c in ctx)
     assert nbytes == 2 * int(ctx.sum()) * 8 * 2 * 2
+
+
+@pytest.mark.parametrize("TD,bpl", [(1, 1), (4, 1), (5, 2), (8, 4), (16, 2), (2, 16), (32, 1), (3, 10)])
+def test_pack_codes_prefix_equality(TD, bpl):
+    # brute force: for every depth r the masked code comparison equals the
+    # level-by-level comparison, and the packing is invertible
+    rng = np.random.default_rng(TD * 100 + bpl)
+    base = 1 << bpl
+    hi = min(base, 3)                     # few distinct values -> many prefix matches
+    a = rng.integers(0, hi, (300, TD))
+    b = a.copy()
+    cut = rng.integers(0, TD + 1, 300)
+    for i in range(300):                  # b agrees with a on a random prefix, then random
+        b[i, cut[i]:] = rng.integers(0, base, TD - cut[i])
+    a[-1] = base - 1                      # extreme values survive packing
+    b[-1] = base - 1
+    ca, cb = od.pack_codes(a, bpl), od.pack_codes(b, bpl)
+    for r in range(TD + 2):
+        m = od.prefix_mask(TD, bpl, r)
+        rr = min(r, TD)
+        want = (a[:, :rr] == b[:, :rr]).all(-1)
+        assert np.array_equal(((ca ^ cb) & m) == 0, want), r
+    for lev in range(TD):
+        shift = bpl * (TD - 1 - lev)
+        got = (ca.astype(np.uint64) >> np.uint64(shift)) & np.uint64(base - 1)
+        assert np.array_equal(got, a[:, lev])
+
+
+def test_pack_codes_rejects_overflowing_levels():
+    with pytest.raises(AssertionError):
+        od.pack_codes(np.array([[4]]), 2)
+    with pytest.raises(AssertionError):
+        od.pack_codes(np.zeros((1, 9)), 4)
