@@ -150,18 +150,51 @@ int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, 
  *             must be zero-filled by the caller (the kernel accumulates with
  *             float atomics, so its low bits depend on the order of the adds).
  * delta       (Z, H, N) fp32 contiguous workspace (rowsum(dout * out)).
+ * plan / n_work / n_multi: the work plan of sa_block_sparse_bwd_plan (same
+ *             lists, shapes and soft bias) and the first two values of its
+ *             plan_info. With a plan, bf16/fp16 inputs with D in {32, 64, 128},
+ *             route_block >= 32, unit stride along D and 16-byte aligned rows
+ *             run on MFMA kernels; otherwise (plan NULL, fp32, other shapes)
+ *             on fp32 FMA kernels.
+ * dkv_partials fp32 workspace of plan_info[2] * 2 * BK * D floats (BK = 128
+ *             when route_block >= 128, else route_block), no initialisation
+ *             needed; NULL when plan_info[1] == 0.
  * dq, dk, dv are fully written (zeros where no pair is visible).
  */
 int sa_block_sparse_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
                         const float* lse, const int32_t* lists, const int32_t* counts, int max_count,
                         const int32_t* t_lists, const int32_t* t_counts, int t_max_count,
                         const void* soft_bias, int soft_bias_dtype, const int64_t* sb_strides,
-                        float* delta, void* dq, void* dk, void* dv, float* d_soft_bias, int Z, int H,
+                        float* delta, void* dq, void* dk, void* dv, float* d_soft_bias,
+                        const void* plan, int n_work, int n_multi, float* dkv_partials, int Z, int H,
                         int H_kv, int N, int D, int route_block, const int64_t* q_strides,
                         const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
                         const int64_t* do_strides, const int64_t* dq_strides, const int64_t* dk_strides,
                         const int64_t* dv_strides, float sm_scale, int dtype, int is_causal,
                         void* stream);
+
+/*
+ * Work plan of the MFMA dK/dV kernel.
+ * Replaces: the grid of _block_list_bwd_dkdv_kernel (one program per key
+ *   block, block_list.py:834-866) and the host read of max(q_counts) in
+ *   build_transposed_block_lists (block_list.py:320): key tiles whose
+ *   transposed lists are long (the sink column is listed by every query
+ *   block) are split into items of a bounded number of entries, placed
+ *   first; the other tiles follow by decreasing entry count.
+ *
+ * Inputs as for sa_block_sparse_bwd. plan: device buffer of at least
+ * sa_block_sparse_bwd_plan_bytes(...) bytes. plan_info: device int32[3]
+ * receiving {work items, split tiles, work items of split tiles}; the caller
+ * reads it back (one device-to-host copy, at the point where the reference
+ * reads max(q_counts)) to size the launch and dkv_partials.
+ * With soft_bias the plan also holds each transposed entry's bias.
+ */
+size_t sa_block_sparse_bwd_plan_bytes(int Z, int H, int H_kv, int N, int route_block, int t_max_count);
+int sa_block_sparse_bwd_plan(const int32_t* lists, const int32_t* counts, int max_count,
+                             const int32_t* t_lists, const int32_t* t_counts, int t_max_count,
+                             const void* soft_bias, int soft_bias_dtype, const int64_t* sb_strides,
+                             int Z, int H, int H_kv, int N, int route_block, void* plan,
+                             size_t plan_bytes, int32_t* plan_info, void* stream);
 
 /*
  * Workspace bytes needed by sa_sparse_paged_decode for B sequences of H query

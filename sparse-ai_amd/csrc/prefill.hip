@@ -27,19 +27,13 @@
 //    [16, 256], any route block: 16 lanes per query row, fp32 FMA math, used
 //    for fp32 inputs (true fp32, no TF32 shortcut) and shapes the MFMA path
 //    does not cover.
-#include "sa_internal.h"
+#include "mfma_util.h"
 
 #include <algorithm>
 #include <type_traits>
 
 namespace sa {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 struct FwdParams {
   const void* q;
@@ -180,66 +174,6 @@ __global__ __launch_bounds__(256) void prefill_generic_kernel(FwdParams p) {
 // ============================================================================
 // MFMA kernel (bf16 / fp16).
 // ============================================================================
-template <typename T> struct Mma;
-template <> struct Mma<bf16_t> {
-  typedef bf16x8_t vec;
-  static __device__ __forceinline__ f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(vec, a),
-                                                   __builtin_bit_cast(vec, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
-};
-template <> struct Mma<f16_t> {
-  typedef f16x8_t vec;
-  static __device__ __forceinline__ f32x16_t mma(u32x4_t a, u32x4_t b, f32x16_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(vec, a),
-                                                  __builtin_bit_cast(vec, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
-};
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt / lgkmcnt left at
-// their "no wait" maxima).
-template <int VM>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(VM >= 0 && VM < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-// Workgroup barrier without the release/acquire fences of __syncthreads():
-// the fence would wait for every in-flight direct-to-LDS load of the
-// pipeline. The kernel orders its own LDS traffic with explicit waits.
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
-
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-#define SA_LDS __attribute__((address_space(3)))
-
-// Direct-to-LDS loads of 16 bytes per lane: lane L's bytes land at LDS
-// address lds_addr + 16 L. Issued through inline asm so that the compiler
-// does not track them: its own wait insertion would otherwise drain every
-// in-flight load before any LDS read. The kernel waits for these loads with
-// explicit vmcnt counts before the barrier that publishes a stage.
-//   dma16:   64-bit per-lane address.
-//   dma16_s: uniform 64-bit base in SGPRs + 32-bit per-lane byte offset.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(lds_addr), "v"(src) : "memory", "m0");
-}
-__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr), "v"(off), "s"(base) : "memory", "m0");
-}
-
-// Wait until at most `ahead` pipeline tiles (LPW loads each) are in flight:
-// `ahead` is the number of tiles issued after the one about to be computed.
-template <int LPW, int MAXA>
-__device__ __forceinline__ void wait_tiles(int ahead) {
-  static_assert(MAXA >= 1 && MAXA <= 3, "pipeline depth");
-  if (MAXA >= 3 && ahead >= 3) wait_vmcnt<3 * LPW>();
-  else if (MAXA >= 2 && ahead >= 2) wait_vmcnt<2 * LPW>();
-  else if (ahead >= 1) wait_vmcnt<LPW>();
-  else wait_vmcnt<0>();
-}
 
 // S: pipeline stages (K+V tiles of BN keys; S - 1 in flight while one is
 // computed). WPE: waves per SIMD the register budget is sized for.

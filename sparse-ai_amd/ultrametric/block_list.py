@@ -254,6 +254,23 @@ def build_transposed_block_lists(
     return block_lists_from_mask(match_kq, sync_free=False)
 
 
+def _transposed_lists_sync_free(lists, counts, max_count, nb):
+    """Transposed lists of width nb (no host read): the layout of
+    build_transposed_block_lists before its cut to max(q_counts)."""
+    Z, H, _ = counts.shape
+    device = lists.device
+    if nb == 0 or max_count == 0:
+        return (torch.zeros((Z, H, nb, 0), dtype=torch.int32, device=device),
+                torch.zeros((Z, H, nb), dtype=torch.int32, device=device), 0)
+    t_idx = torch.arange(max_count, device=device).view(1, 1, 1, max_count)
+    valid = t_idx < counts.unsqueeze(-1)
+    safe_kb = torch.where(valid, lists.to(torch.int64), torch.full_like(lists, nb, dtype=torch.int64))
+    match_qk = torch.zeros((Z, H, counts.shape[2], nb + 1), dtype=torch.bool, device=device)
+    match_qk.scatter_(-1, safe_kb, valid)
+    tl = block_lists_from_mask(match_qk[..., :nb].transpose(-2, -1), sync_free=True)
+    return tl.lists, tl.counts, tl.max_count
+
+
 # ----------------------------------------------------------------------------
 # Forward
 # ----------------------------------------------------------------------------
@@ -374,10 +391,7 @@ def _launch_bwd(dout, q, k, v, out, lse, lists, counts, max_count, soft_block_bi
     dt = nat.dtype_code(q.dtype, (torch.float32, torch.bfloat16, torch.float16))
     if dout.dtype != q.dtype:
         dout = dout.to(q.dtype)
-    t_lists, t_counts, t_max = build_transposed_block_lists(BlockLists(lists, counts, max_count),
-                                                            num_key_blocks=nb)
-    t_lists = t_lists.to(torch.int32).contiguous()
-    t_counts = t_counts.to(torch.int32).contiguous()
+    t_lists, t_counts, t_max = _transposed_lists_sync_free(lists, counts, max_count, nb)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
@@ -390,13 +404,34 @@ def _launch_bwd(dout, q, k, v, out, lse, lists, counts, max_count, soft_block_bi
             sb = sb.float()
         sb_code = nat.DTYPE_CODES[sb.dtype]
         dsb = torch.zeros((Z, H, nb, max_count), dtype=torch.float32, device=dev)
+    lib = nat.lib()
+    lists_p = nat.ptr(lists) if max_count > 0 else None
+    t_lists_p = nat.ptr(t_lists) if t_max > 0 else None
+    sb_st = nat.strides(sb) if sb is not None else None
+    plan, n_work, n_multi, partials = None, 0, 0, None
+    if q.dtype != torch.float32 and route_block >= 32 and Z * H * N > 0:
+        # Work plan of the MFMA dK/dV kernels; its item counts are the one host
+        # read of the backward (the reference reads max(q_counts) at this point,
+        # block_list.py:320).
+        nbytes = int(lib.sa_block_sparse_bwd_plan_bytes(Z, H, Hkv, N, int(route_block), int(t_max)))
+        plan = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        info = torch.empty(3, dtype=torch.int32, device=dev)
+        with torch.cuda.device(dev):
+            rc = lib.sa_block_sparse_bwd_plan(lists_p, nat.ptr(counts), int(max_count), t_lists_p, nat.ptr(t_counts),
+                                              int(t_max), nat.ptr(sb), sb_code, sb_st, Z, H, Hkv, N,
+                                              int(route_block), nat.ptr(plan), nbytes, nat.ptr(info), nat.stream(dev))
+        nat.check(rc)
+        n_work, n_multi, n_multi_items = info.tolist()
+        if n_multi:
+            bk = 128 if route_block >= 128 else route_block
+            partials = torch.empty(n_multi_items * 2 * bk * D, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
-        rc = nat.lib().sa_block_sparse_bwd(
+        rc = lib.sa_block_sparse_bwd(
             nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), nat.ptr(dout), nat.ptr(lse),
-            nat.ptr(lists) if max_count > 0 else None, nat.ptr(counts), int(max_count),
-            nat.ptr(t_lists) if t_max > 0 else None, nat.ptr(t_counts), int(t_max),
-            nat.ptr(sb), sb_code, nat.strides(sb) if sb is not None else None,
+            lists_p, nat.ptr(counts), int(max_count), t_lists_p, nat.ptr(t_counts), int(t_max),
+            nat.ptr(sb), sb_code, sb_st,
             nat.ptr(delta), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dsb),
+            nat.ptr(plan), int(n_work), int(n_multi), nat.ptr(partials),
             Z, H, Hkv, N, D, int(route_block),
             nat.strides(q), nat.strides(k), nat.strides(v), nat.strides(out), nat.strides(dout),
             nat.strides(dq), nat.strides(dk), nat.strides(dv), float(scale), dt, int(bool(is_causal)),

@@ -114,3 +114,80 @@ def test_backward_bf16_gqa(H, Hkv, N, D, rb):
     for g_, r_, name in zip(got, ref[:3], "qkv"):
         scale = max(1.0, np.abs(r_).max())
         assert np.abs(g_ - r_).max() <= 2e-2 * scale, name
+
+
+def pair_bias_of(bias, bl):
+    lists, counts = bl.lists.cpu().numpy(), bl.counts.cpu().numpy()
+    Z, H, NB, _ = bias.shape
+    pb = np.zeros((Z, H, NB, NB))
+    for z in range(Z):
+        for h in range(H):
+            for qb in range(NB):
+                for t in range(counts[z, h, qb]):
+                    pb[z, h, qb, lists[z, h, qb, t]] = bias[z, h, qb, t]
+    return pb
+
+
+def check_grads(got, ref, rel=2e-2):
+    for g_, r_, name in zip(got, ref, "qkv"):
+        scale = max(1.0, np.abs(r_).max())
+        err = np.abs(g_ - r_).max()
+        assert err <= rel * scale, (name, err, scale)
+
+
+# MFMA path: bf16 / fp16, D in {32, 64, 128}, route blocks 32 .. 256 (one to
+# four waves per workgroup, two key tiles per route block at 256), ragged N,
+# soft bias, and sink columns long enough to split a key tile into several
+# work items (fp32 partials summed by the finalize kernel).
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("H,Hkv,N,D,rb,causal,bias", [
+    (2, 2, 1000, 128, 128, True, False),    # ragged tail
+    (4, 1, 2048, 128, 128, True, True),     # sink tile of 4 x 16 entries: 8 items
+    (2, 2, 1536, 64, 64, False, True),      # two waves per workgroup
+    (2, 1, 640, 32, 32, True, False),       # one wave per workgroup
+    (2, 2, 2048, 128, 256, True, True),     # two key tiles per route block
+    (3, 3, 777, 64, 128, False, False),
+])
+def test_backward_mfma(dtype, H, Hkv, N, D, rb, causal, bias):
+    torch.manual_seed(N + D + rb)
+    Z = 1
+    q0, do = (torch.randn(Z, H, N, D).to(dtype) for _ in range(2))
+    k0, v0 = (torch.randn(Z, Hkv, N, D).to(dtype) for _ in range(2))
+    NB = -(-N // rb)
+    router = random_router(Z, H, NB, 3, 2, seed=N + 1).to(DEV)
+    bl = build_block_lists(router, 2, is_causal=causal, sink_block=True, local_blocks=1, arity=2)
+    sb = (torch.randn(Z, H, NB, bl.max_count) * 0.5) if bias else None
+    got = run(q0, k0, v0, do, bl, rb, causal, bias=None if sb is None else sb.to(DEV))
+    ref = oracle(q0, k0, v0, do, bl, rb, causal, pair_bias=None if sb is None else pair_bias_of(sb.numpy(), bl))
+    check_grads(got, ref[:3])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_mfma_soft_bias_ste(causal):
+    # straight-through bias gradient on the MFMA path, with split sink tiles
+    torch.manual_seed(7)
+    Z, H, Hkv, N, D, rb = 1, 4, 2, 1280, 64, 64
+    q0, do = (torch.randn(Z, H, N, D).to(torch.bfloat16) for _ in range(2))
+    k0, v0 = (torch.randn(Z, Hkv, N, D).to(torch.bfloat16) for _ in range(2))
+    NB = N // rb
+    router = random_router(Z, H, NB, 3, 2, seed=23).to(DEV)
+    bl = build_block_lists(router, 1, is_causal=causal, sink_block=True, arity=2)
+    raw = torch.randn(Z, H, NB, bl.max_count, device=DEV, requires_grad=True)
+    ste = raw - raw.detach()
+    q, k, v = (t.to(DEV).clone().requires_grad_(True) for t in (q0, k0, v0))
+    out = block_list_attention(q, k, v, bl, route_block=rb, is_causal=causal, soft_block_bias=ste)
+    out.backward(do.to(DEV))
+    lists, counts = bl.lists.cpu().numpy(), bl.counts.cpu().numpy()
+    bm = ob.lists_to_mask(lists, counts)
+    f = lambda t: t.float().numpy()  # noqa: E731
+    ref = oa.block_sparse_attention_grad_ref(f(q0), f(k0), f(v0), bm, rb, f(do), is_causal=causal,
+                                             pair_bias=np.zeros((Z, H, NB, NB)))
+    want = np.zeros((Z, H, NB, bl.max_count))
+    for h in range(H):
+        for qb in range(NB):
+            for t in range(counts[0, h, qb]):
+                want[0, h, qb, t] = ref[3][0, h, qb, lists[0, h, qb, t]]
+    got = raw.grad.cpu().numpy()
+    assert np.abs(got - want).max() <= 2e-2 * max(1.0, np.abs(want).max())
+    check_grads((q.grad.float().cpu().numpy(), k.grad.float().cpu().numpy(), v.grad.float().cpu().numpy()),
+                ref[:3])
