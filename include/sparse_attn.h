@@ -130,6 +130,23 @@ int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, 
                         int dtype, int is_causal, void* stream);
 
 /*
+ * Transposed block lists: per (z, h, key block), the ascending query blocks
+ * whose lists hold it.
+ * Replaces: build_transposed_block_lists (src/ultrametric/block_list.py:281-327),
+ *   whose scatter / transpose / cumsum steps become one kernel.
+ *
+ * lists / counts / max_count: forward lists (Z, H, NB, max_count) and counts
+ *             (Z, H, NB), int32 contiguous; entries outside [0, NB) are ignored.
+ * t_lists     (Z, H, NB, t_cols) int32 contiguous output, zero-padded; or NULL
+ *             to compute t_counts only (then read max(t_counts) and call again,
+ *             as the reference's max_q_count). Rows longer than t_cols are cut.
+ * t_counts    (Z, H, NB) int32 contiguous output.
+ * Limits: NB <= 512.
+ */
+int sa_transpose_block_lists(const int32_t* lists, const int32_t* counts, int max_count, int Z, int H, int NB,
+                             int32_t* t_lists, int t_cols, int32_t* t_counts, void* stream);
+
+/*
  * Block-sparse attention backward over block lists.
  * Replaces: _block_list_attention_bwd with _block_list_bwd_dq_kernel and
  *   _block_list_bwd_dkdv_kernel (src/ultrametric/block_list.py:758-880,
@@ -159,6 +176,11 @@ int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, 
  * dkv_partials fp32 workspace of plan_info[2] * 2 * BK * D floats (BK = 128
  *             when route_block >= 128, else route_block), no initialisation
  *             needed; NULL when plan_info[1] == 0.
+ * phases      1: delta, dQ and d_soft_bias (the reference's
+ *             _block_list_bwd_dq_kernel); 2: dK and dV (its
+ *             _block_list_bwd_dkdv_kernel), which reads the delta of phase 1;
+ *             3: both. Phase 1 needs no plan, so a caller can queue it before
+ *             reading plan_info back.
  * dq, dk, dv are fully written (zeros where no pair is visible).
  */
 int sa_block_sparse_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
@@ -166,8 +188,8 @@ int sa_block_sparse_bwd(const void* q, const void* k, const void* v, const void*
                         const int32_t* t_lists, const int32_t* t_counts, int t_max_count,
                         const void* soft_bias, int soft_bias_dtype, const int64_t* sb_strides,
                         float* delta, void* dq, void* dk, void* dv, float* d_soft_bias,
-                        const void* plan, int n_work, int n_multi, float* dkv_partials, int Z, int H,
-                        int H_kv, int N, int D, int route_block, const int64_t* q_strides,
+                        const void* plan, int n_work, int n_multi, float* dkv_partials, int phases,
+                        int Z, int H, int H_kv, int N, int D, int route_block, const int64_t* q_strides,
                         const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
                         const int64_t* do_strides, const int64_t* dq_strides, const int64_t* dk_strides,
                         const int64_t* dv_strides, float sm_scale, int dtype, int is_causal,

@@ -405,6 +405,13 @@ __device__ __forceinline__ u32x4_t tr_operand(const char* base, uint32_t r0, uin
   return u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 }
 
+template <typename T> __device__ __forceinline__ float lo_elem(uint32_t w);
+template <typename T> __device__ __forceinline__ float hi_elem(uint32_t w);
+template <> __device__ __forceinline__ float lo_elem<bf16_t>(uint32_t w) { return bf16_bits_to_float(w & 0xffffu); }
+template <> __device__ __forceinline__ float hi_elem<bf16_t>(uint32_t w) { return bf16_bits_to_float(w >> 16); }
+template <> __device__ __forceinline__ float lo_elem<f16_t>(uint32_t w) { return f16_bits_to_float(w & 0xffffu); }
+template <> __device__ __forceinline__ float hi_elem<f16_t>(uint32_t w) { return f16_bits_to_float(w >> 16); }
+
 template <typename T>
 __device__ __forceinline__ u32x4_t pack8(const float* x) {
   return u32x4_t{Mma<T>::pack(x[0], x[1]), Mma<T>::pack(x[2], x[3]), Mma<T>::pack(x[4], x[5]),
@@ -464,7 +471,25 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   }
   const float lse = p.lse[static_cast<int64_t>(zh) * N + qr];
   const float lse2 = lse == -INFINITY ? 0.f : lse * kLog2e;
-  const float delta = p.delta[static_cast<int64_t>(zh) * N + qr];
+  // delta = rowsum(dO * O) in fp32 (lanes kh = 0 / 1 hold the two halves of
+  // the row); stored for the dK / dV kernels.
+  float delta;
+  {
+    const char* orow = reinterpret_cast<const char*>(static_cast<const T*>(p.o) + z * p.os[0] + h * p.os[1] +
+                                                     static_cast<int64_t>(qr) * p.os[2]);
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4_t ov = *reinterpret_cast<const u32x4_t*>(orow + 32 * s + 16 * kh);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        part = fmaf(lo_elem<T>(ov[e]), lo_elem<T>(dof[s][e]), part);
+        part = fmaf(hi_elem<T>(ov[e]), hi_elem<T>(dof[s][e]), part);
+      }
+    }
+    delta = part + __shfl_xor(part, 32);
+    if (qok && kh == 0) p.delta[static_cast<int64_t>(zh) * N + qpos] = delta;
+  }
   const bool want_db = p.sb != nullptr && p.dsb != nullptr;
 
   TP tp;
@@ -889,48 +914,49 @@ void bwd_dkdv_mfma_kernel(BwdParams p) {
   }
 }
 
-// Sums the partials of each split tile's items and writes its dK / dV rows.
+// Sums the partials of each split tile's items and writes its dK / dV rows:
+// workgroup (slot, j) handles float4 column j = (K|V, dt, g) of every lane of
+// the tile's NW waves (coalesced 1-KB reads per wave and item).
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(NW * 64) void bwd_finalize_kernel(BwdParams p) {
-  constexpr int BK = NW * 32, DT = D / 32;
-  const int4 m = p.multi[blockIdx.x];
+  constexpr int BK = NW * 32, DT = D / 32, J = 8 * DT;
+  const int slot = blockIdx.x / J, j = blockIdx.x % J;
+  const int4 m = p.multi[slot];
   const int tile = m.x, first = m.y, nc = m.z;
   const int zk = tile / p.ktiles, nt = tile % p.ktiles;
   const int z = zk / p.Hkv, kvh = zk % p.Hkv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, kh = lane >> 5;
   const int kpos = nt * BK + wave * 32 + li;
+  const f32x4_t* in = reinterpret_cast<const f32x4_t*>(p.partials) + (static_cast<int64_t>(wave) * J + j) * 64 + lane;
+  f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nc; ++c) acc += in[static_cast<int64_t>(first + c) * NW * J * 64];
   if (kpos >= p.N) return;
-  const f32x4_t* in = reinterpret_cast<const f32x4_t*>(p.partials);
-  T* ko = static_cast<T*>(p.dk) + z * p.dks[0] + kvh * p.dks[1] + static_cast<int64_t>(kpos) * p.dks[2];
-  T* vo = static_cast<T*>(p.dv) + z * p.dvs[0] + kvh * p.dvs[1] + static_cast<int64_t>(kpos) * p.dvs[2];
-#pragma unroll
-  for (int j = 0; j < 8 * DT; ++j) {
-    f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < nc; ++c) s += in[((static_cast<int64_t>(first + c) * NW + wave) * 8 * DT + j) * 64 + lane];
-    const int jj = j % (4 * DT), dt = jj >> 2, g = jj & 3;
-    const int d = 32 * dt + 8 * g + 4 * kh;
-    T* o = j < 4 * DT ? ko : vo;
-    *reinterpret_cast<u32x2_t*>(o + d) = u32x2_t{Mma<T>::pack(s[0], s[1]), Mma<T>::pack(s[2], s[3])};
-  }
+  const int jj = j % (4 * DT), dt = jj >> 2, g = jj & 3;
+  const int d = 32 * dt + 8 * g + 4 * kh;
+  T* o = j < 4 * DT
+             ? static_cast<T*>(p.dk) + z * p.dks[0] + kvh * p.dks[1] + static_cast<int64_t>(kpos) * p.dks[2]
+             : static_cast<T*>(p.dv) + z * p.dvs[0] + kvh * p.dvs[1] + static_cast<int64_t>(kpos) * p.dvs[2];
+  *reinterpret_cast<u32x2_t*>(o + d) = u32x2_t{Mma<T>::pack(acc[0], acc[1]), Mma<T>::pack(acc[2], acc[3])};
 }
 
+// Phase 1: dQ (with delta and the soft-bias gradient); phase 2: dK / dV.
 template <typename T, int D, int NW>
-int launch_bwd_mfma_nw(BwdParams& p, hipStream_t s) {
+int launch_dq_mfma_nw(BwdParams& p, hipStream_t s) {
   constexpr int BM = NW * 32;
   p.mtiles = (p.N + BM - 1) / BM;
-  const long long g_delta = (static_cast<long long>(p.Z) * p.H * p.N + 15) / 16;
   const long long g_dq = static_cast<long long>(p.Z) * p.H * p.mtiles;
-  if (g_delta > 0x7fffffffLL || g_dq > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
-  hipLaunchKernelGGL((bwd_delta_kernel<T, D>), dim3(static_cast<unsigned>(g_delta)), dim3(256), 0, s, p);
-  int rc = check_launch("block-sparse backward delta kernel");
-  if (rc != SA_OK) return rc;
+  if (g_dq > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
   if (p.is_causal) {
     hipLaunchKernelGGL((bwd_dq_mfma_kernel<T, D, NW, true>), dim3(static_cast<unsigned>(g_dq)), dim3(NW * 64), 0, s, p);
   } else {
     hipLaunchKernelGGL((bwd_dq_mfma_kernel<T, D, NW, false>), dim3(static_cast<unsigned>(g_dq)), dim3(NW * 64), 0, s, p);
   }
-  rc = check_launch("block-sparse backward dQ (MFMA) kernel");
-  if (rc != SA_OK || p.n_work == 0) return rc;
+  return check_launch("block-sparse backward dQ (MFMA) kernel");
+}
+
+template <typename T, int D, int NW>
+int launch_dkdv_mfma_nw(BwdParams& p, hipStream_t s) {
+  if (p.n_work == 0) return SA_OK;
   if (p.is_causal) {
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, true, 0>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, true, 1>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
@@ -938,24 +964,24 @@ int launch_bwd_mfma_nw(BwdParams& p, hipStream_t s) {
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, false, 0>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, false, 1>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
   }
-  rc = check_launch("block-sparse backward dK/dV (MFMA) kernels");
+  int rc = check_launch("block-sparse backward dK/dV (MFMA) kernels");
   if (rc != SA_OK || p.n_multi == 0) return rc;
-  hipLaunchKernelGGL((bwd_finalize_kernel<T, D, NW>), dim3(p.n_multi), dim3(NW * 64), 0, s, p);
+  hipLaunchKernelGGL((bwd_finalize_kernel<T, D, NW>), dim3(p.n_multi * 8 * (D / 32)), dim3(NW * 64), 0, s, p);
   return check_launch("block-sparse backward dK/dV finalize kernel");
 }
 
 template <typename T, int D>
-int launch_bwd_mfma_d(BwdParams& p, hipStream_t s) {
-  if (p.RB >= 128) return launch_bwd_mfma_nw<T, D, 4>(p, s);
-  if (p.RB == 64) return launch_bwd_mfma_nw<T, D, 2>(p, s);
-  return launch_bwd_mfma_nw<T, D, 1>(p, s);
+int launch_bwd_mfma_d(BwdParams& p, int phase, hipStream_t s) {
+  if (p.RB >= 128) return phase == 1 ? launch_dq_mfma_nw<T, D, 4>(p, s) : launch_dkdv_mfma_nw<T, D, 4>(p, s);
+  if (p.RB == 64) return phase == 1 ? launch_dq_mfma_nw<T, D, 2>(p, s) : launch_dkdv_mfma_nw<T, D, 2>(p, s);
+  return phase == 1 ? launch_dq_mfma_nw<T, D, 1>(p, s) : launch_dkdv_mfma_nw<T, D, 1>(p, s);
 }
 
 template <typename T>
-int launch_bwd_mfma(BwdParams& p, int D, hipStream_t s) {
-  if (D == 32) return launch_bwd_mfma_d<T, 32>(p, s);
-  if (D == 64) return launch_bwd_mfma_d<T, 64>(p, s);
-  return launch_bwd_mfma_d<T, 128>(p, s);
+int launch_bwd_mfma(BwdParams& p, int D, int phase, hipStream_t s) {
+  if (D == 32) return launch_bwd_mfma_d<T, 32>(p, phase, s);
+  if (D == 64) return launch_bwd_mfma_d<T, 64>(p, phase, s);
+  return launch_bwd_mfma_d<T, 128>(p, phase, s);
 }
 
 // Keys per dK/dV work item and transposed entries per item.
@@ -982,30 +1008,31 @@ inline size_t bwd_plan_bytes(int Z, int H, int H_kv, int N, int route_block, int
 }
 
 template <typename T, int D>
-int launch_bwd_d(BwdParams& p, hipStream_t s) {
+int launch_bwd_d(BwdParams& p, int phase, hipStream_t s) {
   const long long rows = static_cast<long long>(p.Z) * p.H * p.N;
   const long long g_delta = (rows + 15) / 16;
   const long long g_dq = static_cast<long long>(p.Z) * p.H * p.tiles;
   const long long g_dkdv = static_cast<long long>(p.Z) * p.Hkv * p.tiles;
   if (g_delta > 0x7fffffffLL || g_dq > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
-  hipLaunchKernelGGL((bwd_delta_kernel<T, D>), dim3(static_cast<unsigned>(g_delta)), dim3(256), 0, s, p);
-  int rc = check_launch("block-sparse backward delta kernel");
-  if (rc != SA_OK) return rc;
-  hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3(static_cast<unsigned>(g_dq)), dim3(256), 0, s, p);
-  rc = check_launch("block-sparse backward dQ kernel");
-  if (rc != SA_OK) return rc;
+  if (phase == 1) {
+    hipLaunchKernelGGL((bwd_delta_kernel<T, D>), dim3(static_cast<unsigned>(g_delta)), dim3(256), 0, s, p);
+    int rc = check_launch("block-sparse backward delta kernel");
+    if (rc != SA_OK) return rc;
+    hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3(static_cast<unsigned>(g_dq)), dim3(256), 0, s, p);
+    return check_launch("block-sparse backward dQ kernel");
+  }
   hipLaunchKernelGGL((bwd_dkdv_kernel<T, D>), dim3(static_cast<unsigned>(g_dkdv)), dim3(256), 0, s, p);
   return check_launch("block-sparse backward dK/dV kernel");
 }
 
 template <typename T>
-int launch_bwd(BwdParams& p, int D, hipStream_t s) {
+int launch_bwd(BwdParams& p, int D, int phase, hipStream_t s) {
   switch (D) {
-    case 16: return launch_bwd_d<T, 16>(p, s);
-    case 32: return launch_bwd_d<T, 32>(p, s);
-    case 64: return launch_bwd_d<T, 64>(p, s);
-    case 128: return launch_bwd_d<T, 128>(p, s);
-    default: return launch_bwd_d<T, 256>(p, s);
+    case 16: return launch_bwd_d<T, 16>(p, phase, s);
+    case 32: return launch_bwd_d<T, 32>(p, phase, s);
+    case 64: return launch_bwd_d<T, 64>(p, phase, s);
+    case 128: return launch_bwd_d<T, 128>(p, phase, s);
+    default: return launch_bwd_d<T, 256>(p, phase, s);
   }
 }
 
@@ -1019,7 +1046,7 @@ extern "C" int sa_block_sparse_bwd(const void* q, const void* k, const void* v, 
                                    int soft_bias_dtype, const int64_t* sb_strides, float* delta,
                                    void* dq, void* dk, void* dv, float* d_soft_bias,
                                    const void* plan, int n_work, int n_multi, float* dkv_partials,
-                                   int Z, int H, int H_kv, int N, int D, int route_block,
+                                   int phases, int Z, int H, int H_kv, int N, int D, int route_block,
                                    const int64_t* q_strides, const int64_t* k_strides,
                                    const int64_t* v_strides, const int64_t* o_strides,
                                    const int64_t* do_strides, const int64_t* dq_strides,
@@ -1065,7 +1092,8 @@ extern "C" int sa_block_sparse_bwd(const void* q, const void* k, const void* v, 
   p.tiles = (N + 15) / 16;
   hipStream_t s = as_stream(stream);
 
-  // MFMA path: unit stride along D, 16-byte aligned rows, and a work plan.
+  // MFMA kernels: unit stride along D and 16-byte aligned rows; dK / dV also
+  // need a work plan.
   bool rows_ok = true;
   for (const int64_t* x : st) rows_ok = rows_ok && x[3] == 1 && x[2] % 8 == 0 && x[1] % 8 == 0 && x[0] % 8 == 0;
   const void* ptrs[8] = {q, k, v, out, dout, dq, dk, dv};
@@ -1073,9 +1101,22 @@ extern "C" int sa_block_sparse_bwd(const void* q, const void* k, const void* v, 
   long long max_rs = 0;
   for (const int64_t* x : st) max_rs = std::max<long long>(max_rs, x[2] * 2);
   const bool offs_ok = N < (1 << 24) && max_rs < (1 << 24) && static_cast<long long>(N) * max_rs < (1LL << 32);
-  const bool mfma_ok = plan != nullptr && dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128) &&
-                       route_block >= 32 && rows_ok && offs_ok;
-  if (mfma_ok) {
+  const bool mfma_shapes = dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128) && route_block >= 32 &&
+                           rows_ok && offs_ok;
+  if (phases < 1 || phases > 3) return fail(SA_EINVAL, "phases must be 1 (dQ), 2 (dK/dV) or 3 (both)");
+  int rc = SA_OK;
+  if (phases & 1) {
+    if (mfma_shapes) {
+      rc = dtype == SA_DTYPE_BF16 ? launch_bwd_mfma<bf16_t>(p, D, 1, s) : launch_bwd_mfma<f16_t>(p, D, 1, s);
+    } else if (dtype == SA_DTYPE_F32) {
+      rc = launch_bwd<float>(p, D, 1, s);
+    } else {
+      rc = dtype == SA_DTYPE_BF16 ? launch_bwd<bf16_t>(p, D, 1, s) : launch_bwd<f16_t>(p, D, 1, s);
+    }
+    if (rc != SA_OK) return rc;
+  }
+  if (!(phases & 2)) return SA_OK;
+  if (mfma_shapes && plan) {
     const int BK = bwd_key_tile(route_block);
     const long long T = static_cast<long long>(Z) * H_kv * ((N + BK - 1) / BK);
     if (n_work < 0 || n_multi < 0 || n_work > T + static_cast<long long>(Z) * H * p.NB * t_max_count) {
@@ -1083,21 +1124,20 @@ extern "C" int sa_block_sparse_bwd(const void* q, const void* k, const void* v, 
     }
     if (n_multi > 0 && !dkv_partials) return fail(SA_EINVAL, "dkv_partials is NULL but the plan has split tiles");
     const char* pl = static_cast<const char*>(plan);
+    const size_t wb = bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max_count);
     p.work = reinterpret_cast<const int4*>(pl);
-    p.multi = reinterpret_cast<const int4*>(pl + bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max_count));
-    p.t_bias = soft_bias ? reinterpret_cast<const float*>(pl + bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max_count) +
-                                                          static_cast<size_t>(T) * sizeof(int4))
-                         : nullptr;
+    p.multi = reinterpret_cast<const int4*>(pl + wb);
+    p.t_bias = soft_bias ? reinterpret_cast<const float*>(pl + wb + static_cast<size_t>(T) * sizeof(int4)) : nullptr;
     p.partials = dkv_partials;
     p.n_work = n_work;
     p.n_multi = n_multi;
     p.ktiles = static_cast<int>((N + BK - 1) / BK);
     p.chunk = bwd_chunk(route_block);
-    return dtype == SA_DTYPE_BF16 ? launch_bwd_mfma<bf16_t>(p, D, s) : launch_bwd_mfma<f16_t>(p, D, s);
+    return dtype == SA_DTYPE_BF16 ? launch_bwd_mfma<bf16_t>(p, D, 2, s) : launch_bwd_mfma<f16_t>(p, D, 2, s);
   }
-  if (dtype == SA_DTYPE_F32) return launch_bwd<float>(p, D, s);
-  if (dtype == SA_DTYPE_BF16) return launch_bwd<bf16_t>(p, D, s);
-  return launch_bwd<f16_t>(p, D, s);
+  if (dtype == SA_DTYPE_F32) return launch_bwd<float>(p, D, 2, s);
+  if (dtype == SA_DTYPE_BF16) return launch_bwd<bf16_t>(p, D, 2, s);
+  return launch_bwd<f16_t>(p, D, 2, s);
 }
 
 extern "C" size_t sa_block_sparse_bwd_plan_bytes(int Z, int H, int H_kv, int N, int route_block, int t_max_count) {

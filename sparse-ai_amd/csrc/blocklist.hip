@@ -230,3 +230,67 @@ extern "C" int sa_build_block_lists_mask(const uint8_t* mask, const int64_t* mas
   p.counts = counts;
   return launch(p, kMask, SA_DTYPE_I32, as_stream(stream));
 }
+
+namespace sa {
+namespace {
+
+constexpr int kTransMaxNB = 512;   // bit matrix of NB x NB bits (+ padding) in 34 KB of LDS
+
+// One workgroup per (z, h): every listed pair (qb, kb) sets bit qb of row kb
+// of an LDS bit matrix (row stride odd, so the row scans below do not share
+// banks); thread kb then writes row kb's query blocks in ascending order,
+// zero-padded to t_cols, and its count.
+__global__ __launch_bounds__(1024) void transpose_lists_kernel(const int32_t* lists, const int32_t* counts,
+                                                               int max_count, int NB, int32_t* t_lists,
+                                                               int t_cols, int32_t* t_counts) {
+  __shared__ uint32_t bits[kTransMaxNB * (kTransMaxNB / 32 + 1)];
+  const int zh = blockIdx.x, tid = threadIdx.x;
+  const int W = (NB + 31) / 32, WS = W | 1;
+  for (int i = tid; i < NB * WS; i += 1024) bits[i] = 0u;
+  __syncthreads();
+  const int32_t* L = lists + static_cast<int64_t>(zh) * NB * max_count;
+  const int32_t* C = counts + static_cast<int64_t>(zh) * NB;
+  for (int i = tid; i < NB * max_count; i += 1024) {
+    const int qb = i / max_count, t = i % max_count;
+    if (t < min(max(C[qb], 0), max_count)) {
+      const int kb = L[i];
+      if (kb >= 0 && kb < NB) atomicOr(&bits[kb * WS + (qb >> 5)], 1u << (qb & 31));
+    }
+  }
+  __syncthreads();
+  for (int kb = tid; kb < NB; kb += 1024) {
+    int n = 0;
+    int32_t* out = t_lists ? t_lists + (static_cast<int64_t>(zh) * NB + kb) * t_cols : nullptr;
+    for (int w = 0; w < W; ++w) {
+      uint32_t x = bits[kb * WS + w];
+      while (x) {
+        const int b = __builtin_ctz(x);
+        x &= x - 1u;
+        if (out && n < t_cols) out[n] = w * 32 + b;
+        ++n;
+      }
+    }
+    if (out) {
+      for (int j = n; j < t_cols; ++j) out[j] = 0;
+    }
+    t_counts[static_cast<int64_t>(zh) * NB + kb] = n;
+  }
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_transpose_block_lists(const int32_t* lists, const int32_t* counts, int max_count, int Z, int H,
+                                        int NB, int32_t* t_lists, int t_cols, int32_t* t_counts, void* stream) {
+  using namespace sa;
+  if (Z < 0 || H < 0 || NB < 0 || max_count < 0 || t_cols < 0) return fail(SA_EINVAL, "negative size");
+  if (NB > kTransMaxNB) return fail(SA_EUNSUPPORTED, "transposed lists need NB <= 512");
+  const long long zh = static_cast<long long>(Z) * H;
+  if (zh == 0 || NB == 0) return SA_OK;
+  if (!counts || !t_counts || (max_count > 0 && !lists)) return fail(SA_EINVAL, "NULL tensor argument");
+  if (t_lists && t_cols < 1) return fail(SA_EINVAL, "t_cols must be >= 1 when t_lists is given");
+  if (zh > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
+  hipLaunchKernelGGL(transpose_lists_kernel, dim3(static_cast<unsigned>(zh)), dim3(1024), 0, as_stream(stream),
+                     lists, counts, max_count, NB, t_lists, t_cols, t_counts);
+  return check_launch("block-list transpose kernel");
+}

@@ -245,6 +245,15 @@ def build_transposed_block_lists(
                           torch.zeros((Z, H, NB_K), dtype=torch.int32, device=device), 0)
     if NB_K != NB_Q:
         raise RuntimeError("build_transposed_block_lists: only square block grids are supported")
+    if NB_Q <= _TRANSPOSE_MAX_NB:
+        l32 = lists.to(torch.int32).contiguous()
+        c32 = counts.to(torch.int32).contiguous()
+        t_counts = torch.empty((Z, H, NB_K), dtype=torch.int32, device=device)
+        _launch_transpose(l32, c32, max_count, None, 0, t_counts)
+        t_max = int(t_counts.max()) if t_counts.numel() else 0     # host read, as block_list.py:320
+        t_lists = torch.empty((Z, H, NB_K, max(t_max, 1)), dtype=torch.int32, device=device)
+        _launch_transpose(l32, c32, max_count, t_lists, max(t_max, 1), t_counts)
+        return BlockLists(t_lists[..., :t_max].contiguous(), t_counts, t_max)
     t_idx = torch.arange(max_count, device=device).view(1, 1, 1, max_count)
     valid = t_idx < counts.unsqueeze(-1)
     safe_kb = torch.where(valid, lists.to(torch.int64), torch.full_like(lists, NB_K, dtype=torch.int64))
@@ -252,6 +261,19 @@ def build_transposed_block_lists(
     match_qk.scatter_(-1, safe_kb, valid)
     match_kq = match_qk[..., :NB_K].transpose(-2, -1)
     return block_lists_from_mask(match_kq, sync_free=False)
+
+
+_TRANSPOSE_MAX_NB = 512   # sa_transpose_block_lists limit; larger grids use torch scatter + compaction
+
+
+def _launch_transpose(lists, counts, max_count, t_lists, t_cols, t_counts):
+    Z, H, NB = counts.shape
+    dev = counts.device
+    with torch.cuda.device(dev):
+        rc = nat.lib().sa_transpose_block_lists(nat.ptr(lists) if max_count > 0 else None, nat.ptr(counts),
+                                                int(max_count), Z, H, NB, nat.ptr(t_lists), int(t_cols),
+                                                nat.ptr(t_counts), nat.stream(dev))
+    nat.check(rc)
 
 
 def _transposed_lists_sync_free(lists, counts, max_count, nb):
@@ -262,6 +284,12 @@ def _transposed_lists_sync_free(lists, counts, max_count, nb):
     if nb == 0 or max_count == 0:
         return (torch.zeros((Z, H, nb, 0), dtype=torch.int32, device=device),
                 torch.zeros((Z, H, nb), dtype=torch.int32, device=device), 0)
+    if nb <= _TRANSPOSE_MAX_NB:
+        t_lists = torch.empty((Z, H, nb, nb), dtype=torch.int32, device=device)
+        t_counts = torch.empty((Z, H, nb), dtype=torch.int32, device=device)
+        _launch_transpose(lists.to(torch.int32).contiguous(), counts.to(torch.int32).contiguous(), max_count,
+                          t_lists, nb, t_counts)
+        return t_lists, t_counts, nb
     t_idx = torch.arange(max_count, device=device).view(1, 1, 1, max_count)
     valid = t_idx < counts.unsqueeze(-1)
     safe_kb = torch.where(valid, lists.to(torch.int64), torch.full_like(lists, nb, dtype=torch.int64))
@@ -408,35 +436,48 @@ def _launch_bwd(dout, q, k, v, out, lse, lists, counts, max_count, soft_block_bi
     lists_p = nat.ptr(lists) if max_count > 0 else None
     t_lists_p = nat.ptr(t_lists) if t_max > 0 else None
     sb_st = nat.strides(sb) if sb is not None else None
-    plan, n_work, n_multi, partials = None, 0, 0, None
-    if q.dtype != torch.float32 and route_block >= 32 and Z * H * N > 0:
-        # Work plan of the MFMA dK/dV kernels; its item counts are the one host
-        # read of the backward (the reference reads max(q_counts) at this point,
-        # block_list.py:320).
-        nbytes = int(lib.sa_block_sparse_bwd_plan_bytes(Z, H, Hkv, N, int(route_block), int(t_max)))
-        plan = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        info = torch.empty(3, dtype=torch.int32, device=dev)
+
+    def launch(phases, plan=None, n_work=0, n_multi=0, partials=None):
         with torch.cuda.device(dev):
-            rc = lib.sa_block_sparse_bwd_plan(lists_p, nat.ptr(counts), int(max_count), t_lists_p, nat.ptr(t_counts),
-                                              int(t_max), nat.ptr(sb), sb_code, sb_st, Z, H, Hkv, N,
-                                              int(route_block), nat.ptr(plan), nbytes, nat.ptr(info), nat.stream(dev))
+            rc = lib.sa_block_sparse_bwd(
+                nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), nat.ptr(dout), nat.ptr(lse),
+                lists_p, nat.ptr(counts), int(max_count), t_lists_p, nat.ptr(t_counts), int(t_max),
+                nat.ptr(sb), sb_code, sb_st,
+                nat.ptr(delta), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dsb),
+                nat.ptr(plan), int(n_work), int(n_multi), nat.ptr(partials), int(phases),
+                Z, H, Hkv, N, D, int(route_block),
+                nat.strides(q), nat.strides(k), nat.strides(v), nat.strides(out), nat.strides(dout),
+                nat.strides(dq), nat.strides(dk), nat.strides(dv), float(scale), dt, int(bool(is_causal)),
+                nat.stream(dev))
         nat.check(rc)
-        n_work, n_multi, n_multi_items = info.tolist()
-        if n_multi:
-            bk = 128 if route_block >= 128 else route_block
-            partials = torch.empty(n_multi_items * 2 * bk * D, dtype=torch.float32, device=dev)
+
+    if q.dtype == torch.float32 or route_block < 32 or Z * H * N == 0:
+        launch(3)
+        return dq, dk, dv, dsb
+    # Work plan of the MFMA dK/dV kernels. Its item counts are the backward's one
+    # host read (the reference reads max(q_counts) at this point, block_list.py:320);
+    # the dQ phase is queued before the read, so the GPU keeps working meanwhile.
+    nbytes = int(lib.sa_block_sparse_bwd_plan_bytes(Z, H, Hkv, N, int(route_block), int(t_max)))
+    plan = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    info = torch.empty(3, dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
-        rc = lib.sa_block_sparse_bwd(
-            nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), nat.ptr(dout), nat.ptr(lse),
-            lists_p, nat.ptr(counts), int(max_count), t_lists_p, nat.ptr(t_counts), int(t_max),
-            nat.ptr(sb), sb_code, sb_st,
-            nat.ptr(delta), nat.ptr(dq), nat.ptr(dk), nat.ptr(dv), nat.ptr(dsb),
-            nat.ptr(plan), int(n_work), int(n_multi), nat.ptr(partials),
-            Z, H, Hkv, N, D, int(route_block),
-            nat.strides(q), nat.strides(k), nat.strides(v), nat.strides(out), nat.strides(dout),
-            nat.strides(dq), nat.strides(dk), nat.strides(dv), float(scale), dt, int(bool(is_causal)),
-            nat.stream(dev))
+        rc = lib.sa_block_sparse_bwd_plan(lists_p, nat.ptr(counts), int(max_count), t_lists_p, nat.ptr(t_counts),
+                                          int(t_max), nat.ptr(sb), sb_code, sb_st, Z, H, Hkv, N,
+                                          int(route_block), nat.ptr(plan), nbytes, nat.ptr(info), nat.stream(dev))
     nat.check(rc)
+    info_host = torch.empty(3, dtype=torch.int32, pin_memory=True)
+    with torch.cuda.device(dev):
+        info_host.copy_(info, non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record()
+    launch(1)
+    ready.synchronize()
+    n_work, n_multi, n_multi_items = info_host.tolist()
+    partials = None
+    if n_multi:
+        bk = 128 if route_block >= 128 else route_block
+        partials = torch.empty(n_multi_items * 2 * bk * D, dtype=torch.float32, device=dev)
+    launch(2, plan, n_work, n_multi, partials)
     return dq, dk, dv, dsb
 
 

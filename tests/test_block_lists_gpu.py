@@ -133,3 +133,15 @@ def test_empty_and_dense_edges():
     r = torch.from_numpy(rand_router(1, 2, 5, 3, 2, seed=0)).to(DEV)
     assert torch.all(build_block_lists(r, 0).counts == 5)
     assert build_block_lists(r, 0, is_causal=True).counts[0, 0].tolist() == [1, 2, 3, 4, 5]
+
+
+@pytest.mark.parametrize("NB,density", [(33, 0.3), (300, 0.05), (512, 0.02), (600, 0.01)])
+def test_transposed_lists_large(NB, density):
+    # the HIP transpose kernel (NB <= 512) and the scatter path above it
+    rng = np.random.default_rng(NB + 1)
+    mask = rng.random((1, 2, NB, NB)) < density
+    mask[..., 0] = True                       # a full sink column
+    bl = block_lists_from_mask(torch.from_numpy(mask).to(DEV), sync_free=False)
+    ref_bl = ob.block_lists_from_mask(mask, sync_free=False)
+    ref = ob.build_transposed_block_lists(ref_bl.lists, ref_bl.counts, NB)
+    assert_same(build_transposed_block_lists(bl, num_key_blocks=NB), ref)
