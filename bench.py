@@ -10,11 +10,12 @@ sum(counts) (every listed 128x128 tile counted in full).
 
 Also reported: the prefill kernel alone (HIP events around back-to-back
 launches on its stream; `roofline` is built from it), the list build alone,
-sparse paged decode on config 4 (GB/s of routed KV bytes), and a CPU
+sparse paged decode on config 4 (GB/s of routed KV bytes), the backward on
+config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), and a CPU
 baseline: the fp32 masked-dense reference (oracle) on the host cores on a
 bounded sample of heads.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-backward]
 Only one GPU is supported: --gpus N > 1 exits with a message.
 """
 
@@ -56,6 +57,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
+    ap.add_argument("--no-backward", action="store_true", help="skip the backward measurement")
     ap.add_argument("--cpu-heads", type=int, default=32, help="heads timed for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU work for the CPU baseline (whole passes over --cpu-heads)")
@@ -278,6 +280,33 @@ def main():
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = src.numel() * src.element_size()
         del src, dst
+
+    # ---------------- config 2 backward (dQ, dK, dV through the public API) ------------
+    if not args.no_backward:
+        from ultrametric.block_list import _launch_bwd
+        with torch.no_grad():
+            out_b, lse_b = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True, return_lse=True)
+        g = torch.Generator(device="cpu").manual_seed(5)
+        dout_b = torch.randn(q.shape, generator=g).to(q.dtype).to(dev)
+        scale_b = 1.0 / math.sqrt(D)
+
+        def bwd():
+            return _launch_bwd(dout_b, q, k, v, out_b, lse_b, bl.lists, bl.counts, bl.max_count, None, RB, True,
+                               scale_b)
+
+        for _ in range(3):
+            bwd()
+        bwd_ms = time_launches(bwd, max(20, args.steps // 5), torch)
+        bwd_flop = 2.5 * flop_alg      # S, dP, dV, dK, dQ: five products of the forward's two
+        result["backward"] = {
+            "workload": "config2 backward: delta + dQ over lists, dK / dV over transposed lists, bf16",
+            "ms_per_call": round(bwd_ms, 5),
+            "flop_alg": bwd_flop,
+            "tflops_alg": round(bwd_flop / (bwd_ms * 1e-3) / 1e12, 1),
+            "includes": "transposed lists, work plan (one host read), all kernels",
+        }
+        log(f"backward {bwd_ms * 1e3:.1f} us/call, {bwd_flop / (bwd_ms * 1e-3) / 1e12:.0f} TFLOP/s algorithmic")
+        del out_b, lse_b, dout_b
 
     # ---------------- config 3: density sweep (optional) ------------------------------
     if args.sweep:

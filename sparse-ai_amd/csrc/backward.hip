@@ -61,9 +61,12 @@ struct BwdParams {
   const int4* work;        // dK/dV work items {tile, chunk, partial slot or -1, entries}
   const int4* multi;       // split tiles {tile, first item, items, 0}
   const float* t_bias;     // soft bias per transposed entry (log2 units) or NULL
+  int2* ent_rh;            // per work item, `chunk` entries {first query row, head}
+  float* ent_b;            // per work item, `chunk` entries: soft bias (log2 units)
   float* partials;         // fp32 dK / dV partials of the items of split tiles
   int n_work, n_multi;
   int ktiles;              // key tiles per (z, kv head)
+  int key_tile;            // keys per key tile
   int chunk;               // transposed entries per work item
   int mtiles;              // query tiles per (z, head) of the dQ kernel
 };
@@ -334,8 +337,12 @@ struct TilePair {
   static constexpr int LPW = 2 * NKI / NW;
   static_assert((2 * NKI) % NW == 0 && LPW >= 1, "loads must split evenly over waves");
   uint32_t goff[LPW];
-  int grow[LPW];
 
+  // Row of the tile that load i of this wave fills (lane dependent).
+  static __device__ __forceinline__ int row_of(int wave, int lane, int i) {
+    const int q = wave * LPW + i;
+    return ((q < NKI ? q : q - NKI) * 64 + lane) / CPR;
+  }
   __device__ __forceinline__ void init(int wave, int lane, uint32_t xsb, uint32_t ysb) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
@@ -343,14 +350,13 @@ struct TilePair {
       const bool isx = q < NKI;
       const int slot = (isx ? q : q - NKI) * 64 + lane;
       const int r = slot / CPR, pos = slot % CPR;
-      grow[i] = r;
       goff[i] = __umul24(static_cast<uint32_t>(r), isx ? xsb : ysb) + 16u * (pos ^ bsw<D>(r));
     }
   }
   // Issues rows row0 .. row0 + 31 of X and Y into LDS at dst (X) / dst + TILEB (Y).
   // Rows outside [0, N) read row N - 1 (or 0); the kernels mask them.
   __device__ __forceinline__ void issue(const char* xb, const char* yb, uint32_t xsb, uint32_t ysb, int row0,
-                                        int N, uint32_t dst, int wave) const {
+                                        int N, uint32_t dst, int wave, int lane) const {
     if (row0 >= 0 && row0 + 32 <= N) {
       const char* xt = xb + static_cast<size_t>(row0) * xsb;
       const char* yt = yb + static_cast<size_t>(row0) * ysb;
@@ -368,8 +374,9 @@ struct TilePair {
         const bool isx = q < NKI;
         const char* gb = isx ? xb : yb;
         const uint32_t rs = isx ? xsb : ysb;
-        const uint32_t rr = static_cast<uint32_t>(min(max(row0 + grow[i], 0), N - 1));
-        const char* src = gb + __umul24(rr, rs) + (goff[i] - __umul24(static_cast<uint32_t>(grow[i]), rs));
+        const int gr = row_of(wave, lane, i);
+        const uint32_t rr = static_cast<uint32_t>(min(max(row0 + gr, 0), N - 1));
+        const char* src = gb + __umul24(rr, rs) + (goff[i] - __umul24(static_cast<uint32_t>(gr), rs));
         const uint32_t d = __builtin_amdgcn_readfirstlane(dst + (isx ? 0 : TILEB) + (isx ? q : q - NKI) * 1024);
         dma16(src, d);
       }
@@ -564,7 +571,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
 #pragma unroll
     for (int st0 = 0; st0 < S - 1; ++st0) {
       key_of[st0] = st0 < total ? tile_key0(st0) : 0;
-      if (st0 < total) tp.issue(kbase, vbase, ksb, vsb, key_of[st0], N, lds_base + st0 * STAGEB, wave);
+      if (st0 < total) tp.issue(kbase, vbase, ksb, vsb, key_of[st0], N, lds_base + st0 * STAGEB, wave, lane);
     }
     key_of[S - 1] = 0;
     int next_key = S - 1 < total ? tile_key0(S - 1) : 0;
@@ -577,7 +584,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
       if (n + S - 1 < total) {
         constexpr int nst = (stg + S - 1) % S;
         key_of[nst] = next_key;
-        tp.issue(kbase, vbase, ksb, vsb, next_key, N, lds_base + nst * STAGEB, wave);
+        tp.issue(kbase, vbase, ksb, vsb, next_key, N, lds_base + nst * STAGEB, wave, lane);
         if (n + S < total) next_key = tile_key0(n + S);
       }
       compute(n, key_of[stg], stg);
@@ -718,8 +725,34 @@ __global__ __launch_bounds__(256) void bwd_tbias_kernel(BwdParams p, float* t_bi
 // PASS 0 accumulates dV (S, P, dV^T += dO^T P; K in registers), PASS 1 dK
 // (S, dP, dS, dK^T += Q^T dS; K and V in registers): one pass holding K, V
 // and both fp32 accumulators would not fit two waves per SIMD at D = 128.
+// Resolves the transposed entries of each work item once (lane e: entry
+// chunk * C + e, walked over the G query heads of the kv head), so that the
+// dK / dV workgroups load them with one read.
+__global__ __launch_bounds__(64) void bwd_items_kernel(BwdParams p) {
+  const int w = blockIdx.x, e = threadIdx.x;
+  const int4 item = p.work[w];
+  const int ne = max(0, min(item.w - item.y * p.chunk, p.chunk));
+  if (e >= ne) return;
+  const int zk = item.x / p.ktiles, nt = item.x % p.ktiles;
+  const int z = zk / p.Hkv, kvh = zk % p.Hkv;
+  const int kb = nt * p.key_tile / p.RB;
+  const int ge = item.y * p.chunk + e;
+  int g = 0, acc = 0;
+  for (; g < p.group - 1; ++g) {
+    const int c = min(max(p.tcounts[(static_cast<int64_t>(z) * p.H + kvh * p.group + g) * p.NB + kb], 0), p.t_max);
+    if (ge < acc + c) break;
+    acc += c;
+  }
+  const int h = kvh * p.group + g;
+  const int64_t trow = (static_cast<int64_t>(z) * p.H + h) * p.NB + kb;
+  const int u = min(max(ge - acc, 0), max(p.t_max - 1, 0));
+  const int64_t slot = static_cast<int64_t>(w) * p.chunk + e;
+  p.ent_rh[slot] = int2{p.tlists[trow * p.t_max + u] * p.RB, h};
+  p.ent_b[slot] = p.t_bias ? p.t_bias[trow * p.t_max + u] : 0.f;
+}
+
 template <typename T, int D, int NW, bool CAUSAL, int PASS>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(PASS == 0 && D != 128 ? 3 : 2)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(PASS == 0 ? 3 : 2)))
 void bwd_dkdv_mfma_kernel(BwdParams p) {
   using TP = TilePair<D, NW>;
   constexpr int S = 3, BK = NW * 32;
@@ -758,22 +791,15 @@ void bwd_dkdv_mfma_kernel(BwdParams p) {
     }
   }
   const int spq = p.RB >> 5, lspq = __builtin_ctz(spq);
-  const int e0 = chunk * p.chunk;
-  const int ne = max(0, min(E - e0, p.chunk));
-  if (tid < ne) {
-    const int e = e0 + tid;
-    int g = 0, acc = 0;
-    for (; g < p.group - 1; ++g) {
-      const int c = min(max(p.tcounts[(static_cast<int64_t>(z) * p.H + kvh * p.group + g) * p.NB + kb], 0), p.t_max);
-      if (e < acc + c) break;
-      acc += c;
-    }
-    const int h = kvh * p.group + g;
-    const int64_t trow = (static_cast<int64_t>(z) * p.H + h) * p.NB + kb;
-    const int u = min(max(e - acc, 0), max(p.t_max - 1, 0));
-    ent_row[tid] = p.tlists[trow * p.t_max + u] * p.RB;
-    ent_h[tid] = h;
-    ent_bias[tid] = p.t_bias ? p.t_bias[trow * p.t_max + u] : 0.f;
+  const int ne = max(0, min(E - chunk * p.chunk, p.chunk));
+  if (tid < p.chunk) {
+    // all `chunk` slots are read (those past ne are never used), so these
+    // loads do not wait for the item header
+    const int64_t slot = static_cast<int64_t>(blockIdx.x) * p.chunk + tid;
+    const int2 rh = p.ent_rh[slot];
+    ent_row[tid] = rh.x;
+    ent_h[tid] = rh.y;
+    ent_bias[tid] = p.ent_b[slot];
   }
   __syncthreads();
   __builtin_amdgcn_s_waitcnt(0);
@@ -790,12 +816,12 @@ void bwd_dkdv_mfma_kernel(BwdParams p) {
 
   auto stage_row = [&](int m) { return ent_row[m >> lspq] + ((m & (spq - 1)) << 5); };
   auto issue = [&](int m, int stg) {
-    const int h = ent_h[m >> lspq];
-    const int row0 = stage_row(m);
+    const int h = __builtin_amdgcn_readfirstlane(ent_h[m >> lspq]);
+    const int row0 = __builtin_amdgcn_readfirstlane(stage_row(m));
     const char* qb0 = reinterpret_cast<const char*>(static_cast<const T*>(p.q) + z * p.qs[0] + h * p.qs[1]);
     const char* db0 = reinterpret_cast<const char*>(static_cast<const T*>(p.dout) + z * p.dos[0] + h * p.dos[1]);
     const uint32_t dst = lds_base + stg * STAGEB;
-    tp.issue(qb0, db0, qsb, dsb, row0, N, dst, wave);
+    tp.issue(qb0, db0, qsb, dsb, row0, N, dst, wave, lane);
     if (lane < LL) {
       const int gl = wave * LL + lane;   // 0..31: lse rows, 32..63: delta rows
       const int r = min(max(row0 + (gl & 31), 0), N - 1);
@@ -957,6 +983,9 @@ int launch_dq_mfma_nw(BwdParams& p, hipStream_t s) {
 template <typename T, int D, int NW>
 int launch_dkdv_mfma_nw(BwdParams& p, hipStream_t s) {
   if (p.n_work == 0) return SA_OK;
+  hipLaunchKernelGGL(bwd_items_kernel, dim3(p.n_work), dim3(64), 0, s, p);
+  int rc0 = check_launch("block-sparse backward work-item kernel");
+  if (rc0 != SA_OK) return rc0;
   if (p.is_causal) {
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, true, 0>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, true, 1>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
@@ -999,12 +1028,18 @@ inline size_t bwd_plan_work_bytes(int Z, int H, int H_kv, int N, int route_block
   const long long C = bwd_chunk(route_block);
   return static_cast<size_t>(T + (entries + C - 1) / C) * sizeof(int4);
 }
+inline size_t bwd_plan_tbias_bytes(int Z, int H, int N, int route_block, int t_max) {
+  const long long NB = (N + route_block - 1) / route_block;
+  return (static_cast<size_t>(Z) * H * NB * t_max * sizeof(float) + 15) / 16 * 16;
+}
+// + the resolved entries of every work item: `chunk` {row, head} pairs and biases.
 inline size_t bwd_plan_bytes(int Z, int H, int H_kv, int N, int route_block, int t_max) {
   const int BK = bwd_key_tile(route_block);
-  const long long NB = (N + route_block - 1) / route_block;
   const long long T = static_cast<long long>(Z) * H_kv * ((N + BK - 1) / BK);
-  return bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max) + static_cast<size_t>(T) * sizeof(int4) +
-         static_cast<size_t>(Z) * H * NB * t_max * sizeof(float);
+  const size_t wb = bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max);
+  const size_t items = wb / sizeof(int4);
+  return wb + static_cast<size_t>(T) * sizeof(int4) + bwd_plan_tbias_bytes(Z, H, N, route_block, t_max) +
+         items * bwd_chunk(route_block) * (sizeof(int2) + sizeof(float));
 }
 
 template <typename T, int D>
@@ -1128,6 +1163,14 @@ extern "C" int sa_block_sparse_bwd(const void* q, const void* k, const void* v, 
     p.work = reinterpret_cast<const int4*>(pl);
     p.multi = reinterpret_cast<const int4*>(pl + wb);
     p.t_bias = soft_bias ? reinterpret_cast<const float*>(pl + wb + static_cast<size_t>(T) * sizeof(int4)) : nullptr;
+    {
+      char* rec = const_cast<char*>(pl) + wb + static_cast<size_t>(T) * sizeof(int4) +
+                  bwd_plan_tbias_bytes(Z, H, N, route_block, t_max_count);
+      const size_t items = wb / sizeof(int4);
+      p.ent_rh = reinterpret_cast<int2*>(rec);
+      p.ent_b = reinterpret_cast<float*>(rec + items * bwd_chunk(route_block) * sizeof(int2));
+    }
+    p.key_tile = BK;
     p.partials = dkv_partials;
     p.n_work = n_work;
     p.n_multi = n_multi;

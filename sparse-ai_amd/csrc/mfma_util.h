@@ -59,9 +59,16 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds_addr), "v"(src) : "memory", "m0");
 }
+// A pointer that is the same in every lane, moved to scalar registers.
+__device__ __forceinline__ const char* uniform_ptr(const char* x) {
+  const uint64_t v = reinterpret_cast<uint64_t>(x);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 __device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr), "v"(off), "s"(base) : "memory", "m0");
+               :: "s"(lds_addr), "v"(off), "s"(uniform_ptr(static_cast<const char*>(base))) : "memory", "m0");
 }
 
 // Wait until at most `ahead` pipeline tiles (LPW loads each) are in flight:
