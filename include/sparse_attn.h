@@ -301,6 +301,49 @@ int sa_sparse_paged_decode_codes(const void* q, const void* k_cache, const void*
                                  int dtype, void* stream);
 
 /*
+ * Ternary (2-bit) quantize + pack of rows.
+ * Replaces: TernaryQuantize + pack_ternary (src/llama_surgery/surgery.py:15-55).
+ *
+ * x           (rows, D) of dtype (F32/BF16/F16), strides[2] (row, element).
+ * mode        0: gamma = mean |x| of the row; x > gamma/2 -> +1,
+ *             x < -gamma/2 -> -1, else 0 (TernaryQuantize); scale = gamma.
+ *             1: x already in {-1, 0, 1} (pack_ternary); scale = 1.
+ * packed      (rows, D / 16) int32 contiguous: value i of word w in bits
+ *             [2i, 2i + 2) of word w, code 0 -> 0, 1 -> +1, 2 -> -1.
+ * scale       optional (rows,) fp32 contiguous.
+ * Limits: D % 16 == 0.
+ */
+int sa_ternary_pack(const void* x, int dtype, const int64_t* strides, int rows, int D, int mode,
+                    int32_t* packed, float* scale, void* stream);
+
+/*
+ * Causal block-sparse prefill over ternary packed K / V.
+ * Replaces: _ternary_ultrametric_fwd_kernel and ternary_ultrametric_attention_triton
+ *   (src/llama_surgery/kernel.py:147-249, :348-420), run over block lists
+ *   (route block 128) that carry its block choice (routing match on the first
+ *   req_depth levels, sink, local window, causal); GQA added.
+ *
+ * q, out      (Z, H, N, D) fp16, strides[4] (unit along D, 16-byte aligned rows).
+ * k_packed, v_packed (Z, H_kv, N, D / 16) int32 (unit stride along the last dim),
+ *             strides[4]; k_scale, v_scale (Z, H_kv, N) of scale_dtype, strides[3].
+ *             Key j's vectors are unpack(k_packed[j]) * k_scale[j], and so for v.
+ * lists / counts / max_count: block lists for route block 128 (is_causal,
+ *             sink and local band applied).
+ * shift_size  keys and queries interact only on the same side of
+ *             N - shift_size (the reference's region mask).
+ * Scale 1/sqrt(D); rows with no visible key get 0 (the reference yields NaN
+ * for a row whose first visited block has no visible key).
+ * Limits: D in {32, 64, 128}.
+ */
+int sa_ternary_prefill_fwd(const void* q, const int32_t* k_packed, const int32_t* v_packed,
+                           const void* k_scale, const void* v_scale, int scale_dtype,
+                           const int32_t* lists, const int32_t* counts, int max_count, void* out,
+                           int Z, int H, int H_kv, int N, int D, int shift_size,
+                           const int64_t* q_strides, const int64_t* kp_strides, const int64_t* vp_strides,
+                           const int64_t* ks_strides, const int64_t* vs_strides, const int64_t* o_strides,
+                           void* stream);
+
+/*
  * Route-block majority vote of the surgery caller.
  * Replaces: the per-level majority vote of token argmax branches in
  *   SurgicalLlamaAttention._block_list_prefill

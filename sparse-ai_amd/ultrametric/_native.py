@@ -49,6 +49,9 @@ _SIGNATURES = {
                                  _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _I64P, _I64P, _I64P, _I64P,
                                  _I64P, _I64P, _I64P, _I64P, ctypes.c_float, _I, _I, _P]),
     "sa_transpose_block_lists": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _P, _P]),
+    "sa_ternary_pack": (_I, [_P, _I, _I64P, _I, _I, _I, _P, _P, _P]),
+    "sa_ternary_prefill_fwd": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
+                                    _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _P]),
     "sa_block_sparse_bwd_plan_bytes": (ctypes.c_size_t, [_I, _I, _I, _I, _I, _I]),
     "sa_block_sparse_bwd_plan": (_I, [_P, _P, _I, _P, _P, _I, _P, _I, _I64P, _I, _I, _I, _I, _I, _P,
                                       ctypes.c_size_t, _P, _P]),
