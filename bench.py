@@ -11,11 +11,11 @@ sum(counts) (every listed 128x128 tile counted in full).
 Also reported: the prefill kernel alone (HIP events around back-to-back
 launches on its stream; `roofline` is built from it), the list build alone,
 sparse paged decode on config 4 (GB/s of routed KV bytes), the backward on
-config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), and a CPU
-baseline: the fp32 masked-dense reference (oracle) on the host cores on a
+config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), the
+ternary packed-K/V prefill over config 2's lists, and a CPU baseline: the fp32 masked-dense reference (oracle) on the host cores on a
 bounded sample of heads.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-backward]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-backward] [--no-ternary]
 Only one GPU is supported: --gpus N > 1 exits with a message.
 """
 
@@ -58,6 +58,7 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward measurement")
+    ap.add_argument("--no-ternary", action="store_true", help="skip the ternary packed-K/V measurement")
     ap.add_argument("--cpu-heads", type=int, default=32, help="heads timed for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU work for the CPU baseline (whole passes over --cpu-heads)")
@@ -307,6 +308,33 @@ def main():
         }
         log(f"backward {bwd_ms * 1e3:.1f} us/call, {bwd_flop / (bwd_ms * 1e-3) / 1e12:.0f} TFLOP/s algorithmic")
         del out_b, lse_b, dout_b
+
+    # ---------------- ternary packed K / V over config 2's lists -------------------------
+    if not args.no_ternary:
+        from ultrametric import ternary_quantize_pack
+        qh = q.half()
+        kp, ksc = ternary_quantize_pack(k)
+        vp, vsc = ternary_quantize_pack(v)
+        tout = torch.empty_like(qh)
+        targs = (nat.ptr(qh), nat.ptr(kp), nat.ptr(vp), nat.ptr(ksc), nat.ptr(vsc), 0, nat.ptr(lists),
+                 nat.ptr(counts), bl.max_count, nat.ptr(tout), Z, H, H, N, D, 0, nat.strides(qh), nat.strides(kp),
+                 nat.strides(vp), nat.strides(ksc), nat.strides(vsc), nat.strides(tout), stream)
+        tfn = nat.lib().sa_ternary_prefill_fwd
+
+        def tern():
+            nat.check(tfn(*targs))
+
+        tern_ms = time_launches(tern, max(50, args.steps), torch)
+        result["ternary"] = {
+            "workload": "config2 lists, fp16 Q, K / V quantized to 2-bit ternary codes + fp32 row scales "
+                        "(64 B per key row instead of 512)",
+            "ms_per_call": round(tern_ms, 5),
+            "tflops": round(flop_alg / (tern_ms * 1e-3) / 1e12, 1),
+            "kv_bytes": kp.numel() * 4 * 2 + ksc.numel() * 4 * 2,
+            "kv_bytes_bf16": k.numel() * 2 * 2,
+        }
+        log(f"ternary prefill {tern_ms * 1e3:.1f} us, {flop_alg / (tern_ms * 1e-3) / 1e12:.0f} TFLOP/s")
+        del qh, kp, vp, ksc, vsc, tout
 
     # ---------------- config 3: density sweep (optional) ------------------------------
     if args.sweep:

@@ -66,15 +66,29 @@ __device__ __forceinline__ float load_scale(const void* base, int dtype, int64_t
   return Elem<f16_t>::load(static_cast<const f16_t*>(base) + off);
 }
 
-// fp16 bits of the 2-bit codes 0..3: 0, +1, -1, +3.
-__device__ __forceinline__ uint32_t code_h(uint32_t c) {
-  return static_cast<uint32_t>((0x4200BC003C000000ull >> (16u * c)) & 0xffffu);
+// Unpacks one word (16 codes) into 8 words of fp16 pairs: out[j] holds values
+// 2j (low half) and 2j + 1. The fp16 bits of codes 0..3 (0, +1, -1, +3) differ
+// in their high byte only, so a byte permute (v_perm_b32) with the table
+// 0x42BC3C00 maps a selector [0x0C, code, 0x0C, code] (0x0C selects a zero
+// byte) to one output word. Selectors come from the codes split into bytes:
+// E0 / E1 / O0 / O1 hold codes 4b / 4b+2 / 4b+1 / 4b+3 in byte b.
+__device__ __forceinline__ void unpack_word(uint32_t w, uint32_t (&out)[8]) {
+  const uint32_t E = w & 0x33333333u, O = (w >> 2) & 0x33333333u;
+  const uint32_t E0 = E & 0x0F0F0F0Fu, E1 = (E >> 4) & 0x0F0F0F0Fu;
+  const uint32_t O0 = O & 0x0F0F0F0Fu, O1 = (O >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t b = static_cast<uint32_t>(j >> 1);
+    const uint32_t S = 0x0Cu | (b << 8) | (0x0Cu << 16) | ((4u + b) << 24);
+    const uint32_t sel = __builtin_amdgcn_perm(j & 1 ? O1 : O0, j & 1 ? E1 : E0, S) | 0x000C000Cu;
+    out[j] = __builtin_amdgcn_perm(0u, 0x42BC3C00u, sel);
+  }
 }
 
 constexpr int kTernSeg = 256;
 
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void ternary_prefill_kernel(TernParams p) {
   constexpr int BN = 32, RB = 128, WPR = D / 16;   // packed words per row
   constexpr int ROWB = 2 * D, TILEB = BN * ROWB, STAGEB = 2 * TILEB + 256;
@@ -116,42 +130,41 @@ void ternary_prefill_kernel(TernParams p) {
   const int32_t* kp0 = p.kp + z * p.kps0 + kvh * p.kps1;
   const int32_t* vp0 = p.vp + z * p.vps0 + kvh * p.vps1;
   const int64_t ks0 = z * p.kss0 + kvh * p.kss1, vs0 = z * p.vss0 + kvh * p.vss1;
-  uint32_t kw = 0, vw = 0;
-  float sc = 0.f;
-  auto load_tile = [&](int key0) {
+  // Two register sets: the words of a tile are loaded two stages before they
+  // are unpacked into LDS.
+  uint32_t kw[2] = {0u, 0u}, vw[2] = {0u, 0u};
+  float sc[2] = {0.f, 0.f};
+  auto load_tile = [&](int key0, int r) {
     const int key = min(max(key0 + lr, 0), N - 1);
     if (loads_word) {
-      kw = static_cast<uint32_t>(kp0[key * p.kps2 + lw]);
-      vw = static_cast<uint32_t>(vp0[key * p.vps2 + lw]);
+      kw[r] = static_cast<uint32_t>(kp0[key * p.kps2 + lw]);
+      vw[r] = static_cast<uint32_t>(vp0[key * p.vps2 + lw]);
     }
     if (tid < 64) {
       const int sk = min(max(key0 + (tid & 31), 0), N - 1);
-      sc = tid < 32 ? load_scale(p.ks, p.scale_dtype, ks0 + sk * p.kss2)
-                    : load_scale(p.vs, p.scale_dtype, vs0 + sk * p.vss2);
+      sc[r] = tid < 32 ? load_scale(p.ks, p.scale_dtype, ks0 + sk * p.kss2)
+                       : load_scale(p.vs, p.scale_dtype, vs0 + sk * p.vss2);
     }
   };
-  // Unpacks the loaded words into stage `stg`: word lw of row lr covers
+  // Unpacks register set r into stage `stg`: word lw of row lr covers
   // d = 16 lw .. 16 lw + 15, i.e. chunks 2 lw and 2 lw + 1.
-  auto store_tile = [&](int stg) {
+  auto store_tile = [&](int stg, int r) {
     char* base = stage_lds + stg * STAGEB;
     if (loads_word) {
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
-        const uint32_t w = t2 == 0 ? kw : vw;
+        const uint32_t w = t2 == 0 ? kw[r] : vw[r];
         char* tile = base + t2 * TILEB + lr * ROWB;
+        uint32_t u[8];
+        unpack_word(w, u);
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          u32x4_t c;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = 8 * half + 2 * e;
-            c[e] = code_h((w >> (2 * i)) & 3u) | (code_h((w >> (2 * i + 2)) & 3u) << 16);
-          }
-          *reinterpret_cast<u32x4_t*>(tile + 16 * ((2 * lw + half) ^ tsw<D>(lr))) = c;
+          *reinterpret_cast<u32x4_t*>(tile + 16 * ((2 * lw + half) ^ tsw<D>(lr))) =
+              u32x4_t{u[4 * half], u[4 * half + 1], u[4 * half + 2], u[4 * half + 3]};
         }
       }
     }
-    if (tid < 64) reinterpret_cast<float*>(base + 2 * TILEB)[tid] = sc;
+    if (tid < 64) reinterpret_cast<float*>(base + 2 * TILEB)[tid] = sc[r];
   };
 
   uint32_t rm[KS];
@@ -186,12 +199,10 @@ void ternary_prefill_kernel(TernParams p) {
     // that touch the shifted region
     const bool need_mask = key0 + BN > N || key0 + BN - 1 > qw0 ||
                            (p.shift > 0 && (key0 + BN > split || qw0 + 31 >= split));
-    float s2[16], vsc[16];
     float mx = -INFINITY;
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const f32x4_t k4 = *reinterpret_cast<const f32x4_t*>(sbase + 2 * TILEB + 4 * (8 * g4 + 4 * kh));
-      const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(sbase + 2 * TILEB + 128 + 4 * (8 * g4 + 4 * kh));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int v = 4 * g4 + i;
@@ -200,8 +211,7 @@ void ternary_prefill_kernel(TernParams p) {
           const int key = key0 + 8 * g4 + 4 * kh + i;
           if (key >= N || key > qpos || ((key >= split) != qtail)) x = -INFINITY;
         }
-        s2[v] = x;
-        vsc[v] = v4[i];
+        st[v] = x;
         mx = fmaxf(mx, x);
       }
     }
@@ -220,10 +230,15 @@ void ternary_prefill_kernel(TernParams p) {
     m_i = m_new;
     float pv[16];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float e = fast_exp2(s2[v] - m_ref);
-      l_i += e;
-      pv[v] = e * vsc[v];
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(sbase + 2 * TILEB + 128 + 4 * (8 * g4 + 4 * kh));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int v = 4 * g4 + i;
+        const float e = fast_exp2(st[v] - m_ref);
+        l_i += e;
+        pv[v] = e * v4[i];
+      }
     }
     u32x4_t pb[2];
 #pragma unroll
@@ -251,17 +266,24 @@ void ternary_prefill_kernel(TernParams p) {
     __syncthreads();
     const int total = seg_n * (RB / BN);
     auto key_of = [&](int n) { return list_lds[n >> 2] * RB + (n & 3) * BN; };
-    load_tile(key_of(0));
-    store_tile(0);
-    if (total > 1) load_tile(key_of(1));
+    // register set / LDS stage of tile n: n & 1
+    load_tile(key_of(0), 0);
+    if (total > 1) load_tile(key_of(1), 1);
+    store_tile(0, 0);
+    if (total > 2) load_tile(key_of(2), 0);
     __syncthreads();
-    for (int n = 0; n < total; ++n) {
-      compute(key_of(n), n & 1);
+    auto step = [&](int n, auto par_c) {
+      constexpr int par = decltype(par_c)::value;   // n & 1
+      compute(key_of(n), par);
       if (n + 1 < total) {
-        store_tile((n + 1) & 1);
-        if (n + 2 < total) load_tile(key_of(n + 2));
+        store_tile(par ^ 1, par ^ 1);
+        if (n + 3 < total) load_tile(key_of(n + 3), par ^ 1);
       }
       __syncthreads();
+    };
+    for (int n = 0; n < total; n += 2) {
+      step(n, std::integral_constant<int, 0>{});
+      if (n + 1 < total) step(n + 1, std::integral_constant<int, 1>{});
     }
   }
 
