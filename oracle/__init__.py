@@ -13,9 +13,12 @@ Modules:
                pairwise block-mask reference, transposed lists.
   attention  — token masks and masked-dense attention (out and LSE), float64
                numpy, plus the fp32 torch variant timed as the CPU baseline.
-  decode     — sparse paged decode reference (GQA by head grouping).
+  decode     — sparse paged decode reference (GQA by head grouping), and
+               the packed per-page routing codes.
   surgery    — the surgery caller's route-block majority vote and its
                allowed-key statistics.
+  ternary    — ternary quantize / pack / unpack and the causal block-sparse
+               prefill over packed K / V (llama_surgery).
 
 Parity pinning: see the header of each module for the checks that pin it
 (known-answer tests from the reference's own tests, closed forms, brute

@@ -21,7 +21,7 @@ from .block_list import (
 )
 from .kernel import block_sparse_attention, routing_to_block_indices
 from .kernel_decode import pack_routing_codes, ultrametric_decode, ultrametric_decode_packed
-from .surgery import block_list_prefill, route_block_vote
+from .surgery import RouteCache, block_list_prefill, route_block_vote
 from .ternary import pack_ternary, ternary_quantize_pack, ternary_ultrametric_attention
 
 __all__ = [
@@ -40,6 +40,7 @@ __all__ = [
     "ultrametric_decode_packed",
     "route_block_vote",
     "block_list_prefill",
+    "RouteCache",
     "ternary_quantize_pack",
     "pack_ternary",
     "ternary_ultrametric_attention",

@@ -36,7 +36,7 @@ import torch
 from . import _native as nat
 from .block_list import block_list_attention, build_block_lists
 
-__all__ = ["route_block_vote", "block_list_prefill", "local_blocks_of"]
+__all__ = ["route_block_vote", "block_list_prefill", "local_blocks_of", "RouteCache"]
 
 _SCORE_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -69,10 +69,41 @@ def route_block_vote(assignments: torch.Tensor, r: int, route_block: int) -> tor
     return out
 
 
+class RouteCache:
+    """Cross-layer reuse of routing (surgery.py:295-315, ``surgical_route_stride``).
+
+    With ``stride`` s > 1, layer l with l % s != 0 reuses the block lists of its
+    anchor layer (l // s) * s, provided the anchor was built with the same
+    (B, H, NB, r, route_block, local_window, p); the reference caches the
+    anchor's routing assignments under the same rule, this cache keeps the
+    anchor's block lists, so that non-anchor layers launch neither the vote
+    nor the list build. Anchor layers always route and store their lists.
+    """
+
+    def __init__(self, stride: int = 1):
+        self.stride = max(1, int(stride))
+        self._lists = {}
+
+    def clear(self):
+        self._lists.clear()
+
+    def lookup(self, layer_idx: int, key: tuple):
+        if self.stride > 1 and layer_idx % self.stride != 0:
+            hit = self._lists.get((layer_idx // self.stride) * self.stride)
+            if hit is not None and hit[0] == key:
+                return hit[1]
+        return None
+
+    def store(self, layer_idx: int, key: tuple, lists):
+        if layer_idx % self.stride == 0:
+            self._lists[layer_idx] = (key, lists)
+
+
 def block_list_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, assignments: torch.Tensor, r: int,
                        *, p: int, route_block: int = 128, local_window: int = 16,
                        sm_scale: Optional[float] = None, block_assignments: Optional[torch.Tensor] = None,
-                       return_stats: bool = False):
+                       return_stats: bool = False, route_cache: Optional[RouteCache] = None,
+                       layer_idx: Optional[int] = None):
     """Causal block-list prefill with block-granular tree routing.
 
     q: (B, H, S, D); k, v: (B, H_kv, S, D). ``assignments``: (B, H, S, L, p)
@@ -81,19 +112,28 @@ def block_list_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, assign
     (B, H, NB, L, p) take precedence, as in the reference. ``r``: routed
     levels (req_depth). Returns the attention output, plus a dict with
     ``mean_allowed_keys``, ``mean_causal_keys`` and ``block_density``
-    (surgery.py:589-595; host reads) when ``return_stats``.
+    (surgery.py:589-595; host reads) when ``return_stats``. With ``route_cache``
+    and ``layer_idx``, non-anchor layers reuse their anchor's lists (see
+    RouteCache) and ``assignments`` is not read for them.
     """
     B, H, S, _ = q.shape
     RB = int(route_block)
     NB = -(-S // RB)
-    if block_assignments is not None and block_assignments.shape[2] == NB:
-        route = route_block_vote(block_assignments[:, :, :NB], r, 1)
-    elif assignments.shape[2] == NB and NB != S:
-        route = route_block_vote(assignments[:, :, :NB], r, 1)
-    else:
-        route = route_block_vote(assignments[:, :, :S], r, RB)
-    bl = build_block_lists(route, r, is_causal=True, sink_block=True,
-                           local_blocks=local_blocks_of(local_window, RB), arity=p)
+    key = (B, H, NB, int(r), RB, int(local_window), int(p))
+    bl = None
+    if route_cache is not None and layer_idx is not None:
+        bl = route_cache.lookup(int(layer_idx), key)
+    if bl is None:
+        if block_assignments is not None and block_assignments.shape[2] == NB:
+            route = route_block_vote(block_assignments[:, :, :NB], r, 1)
+        elif assignments.shape[2] == NB and NB != S:
+            route = route_block_vote(assignments[:, :, :NB], r, 1)
+        else:
+            route = route_block_vote(assignments[:, :, :S], r, RB)
+        bl = build_block_lists(route, r, is_causal=True, sink_block=True,
+                               local_blocks=local_blocks_of(local_window, RB), arity=p)
+        if route_cache is not None and layer_idx is not None:
+            route_cache.store(int(layer_idx), key, bl)
     out = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True, sm_scale=sm_scale)
     if not return_stats:
         return out

@@ -91,3 +91,24 @@ def test_block_list_prefill_gqa_bf16_direct_blocks():
     ref, _ = oa.block_sparse_attention_ref(q.float().numpy(), k.float().numpy(), v.float().numpy(), mask, rb,
                                            is_causal=True)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-2
+
+
+def test_route_cache_reuses_anchor_lists():
+    # stride 2: layers 1 and 3 reuse the lists of anchors 0 and 2 and never read their own scores
+    from ultrametric import RouteCache
+    torch.manual_seed(21)
+    B, H, S, D, L, p, rb, r = 1, 4, 2048, 64, 3, 2, 128, 2
+    q, k, v = (torch.randn(B, H, S, D).to(torch.bfloat16).to(DEV) for _ in range(3))
+    a0, a1 = (torch.randn(B, H, S, L, p).to(DEV) for _ in range(2))
+    cache = RouteCache(stride=2)
+    kw = dict(p=p, route_block=rb, local_window=16)
+    fresh0 = block_list_prefill(q, k, v, a0, r, **kw)
+    fresh1 = block_list_prefill(q, k, v, a1, r, **kw)
+    assert not torch.equal(fresh0, fresh1)
+    assert torch.equal(block_list_prefill(q, k, v, a0, r, route_cache=cache, layer_idx=0, **kw), fresh0)
+    assert torch.equal(block_list_prefill(q, k, v, a1, r, route_cache=cache, layer_idx=1, **kw), fresh0)
+    assert torch.equal(block_list_prefill(q, k, v, a1, r, route_cache=cache, layer_idx=2, **kw), fresh1)
+    assert torch.equal(block_list_prefill(q, k, v, a0, r, route_cache=cache, layer_idx=3, **kw), fresh1)
+    # a different routing depth is a different key: layer 3 routes by itself
+    got = block_list_prefill(q, k, v, a0, 1, route_cache=cache, layer_idx=3, **kw)
+    assert torch.equal(got, block_list_prefill(q, k, v, a0, 1, **kw))
