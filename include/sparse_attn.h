@@ -261,6 +261,33 @@ int sa_sparse_paged_decode(const void* q, const void* k_cache, const void* v_cac
                            int dtype, void* stream);
 
 /*
+ * Sparse paged decode selecting pages by packed routing codes stored per
+ * sequence in logical page order.
+ * Extension of ultrametric_decode (kernel_decode.py:22-124, :188-247): the
+ *   serving-side page-routing format. seq_codes (B, H, max_pages) of
+ *   code_bytes-byte unsigned codes (1, 2 or 4; TD * bits_per_level must fit),
+ *   strides sc_strides[3] in codes: seq_codes[b, h, l] = the packed code
+ *   (sa_pack_page_codes) of the physical page block_tables[b, l] for head h,
+ *   written once when the page is appended. A workgroup then reads its heads'
+ *   codes as contiguous rows, in the same round trip as the block table,
+ *   instead of one scattered row per physical page. Entries past a
+ *   sequence's pages are not read for selection.
+ *   q_codes (B, H) uint32, strides qc_strides[2]. Other arguments as
+ *   sa_sparse_paged_decode_codes; same results.
+ */
+int sa_sparse_paged_decode_seq_codes(const void* q, const void* k_cache, const void* v_cache,
+                                     const int32_t* block_tables, const int32_t* context_lens,
+                                     const void* seq_codes, int code_bytes, const uint32_t* q_codes,
+                                     void* out, int B, int H, int H_kv, int D, int page_size, int TD,
+                                     int bits_per_level, int max_pages, int num_phys_pages,
+                                     int req_depth, int local_blocks, int sink_block,
+                                     const int64_t* q_strides, const int64_t* k_strides,
+                                     const int64_t* v_strides, const int64_t* bt_strides,
+                                     const int64_t* sc_strides, const int64_t* qc_strides,
+                                     const int64_t* o_strides, void* workspace, size_t workspace_bytes,
+                                     int dtype, void* stream);
+
+/*
  * Packs routing levels into one 32-bit code per (row, head).
  * Extension of ultrametric_decode (src/ultrametric/kernel_decode.py:22-124,
  *   whose kernel re-reads TD int32 levels per (page, head), :76-81): the

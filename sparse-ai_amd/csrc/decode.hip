@@ -58,7 +58,11 @@ struct DecParams {
   int vec_router;  // router rows allow one 16-byte load of 4 levels per (page, head)
   const uint32_t* codes;    // packed mode: (P, H) page routing codes, or NULL
   const uint32_t* qcodes;   // packed mode: (B, H) query routing codes
-  int64_t cs0, cs1, qcs0, qcs1;
+  int64_t cs0, cs1, cs2, qcs0, qcs1;
+  int lvec;                 // logical codes: rows allow 2 x 16-byte loads per 8 pages
+  int logical;              // codes are (B, H, max_pages) in logical page order
+  int code_bytes;           // logical codes: 1, 2 or 4 bytes per code
+  const void* lcodes;       // logical codes (element size code_bytes)
   uint32_t code_mask;       // bits of the first r levels (0 when r == 0)
   int64_t qs0, qs1, qs2;
   int64_t ks0, ks1, ks2;
@@ -141,19 +145,29 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t ballot) {
                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ballot), 0u));
 }
 
-template <typename T, int D, int G>
+// MODE 0: int32 routing levels per (physical page, head) (the reference's
+// router). MODE 1: packed routing codes per (physical page, head); the
+// phase-A registers are then small enough for 2048-page ranges at G >= 4.
+// MODE 2: packed codes per (sequence, head, logical page): a workgroup's codes
+// are contiguous, so thread t reads the codes and block-table entries of
+// pages 8t .. 8t+7 of a 2048-page range with wide loads issued in the
+// prologue, and builds their head masks in registers (no ballot).
+template <typename T, int D, int G, int MODE>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(G * D <= 512 ? 2 : 1)))
 void decode_kernel(DecParams p) {
+  constexpr bool PACKED = MODE == 1;
+  constexpr bool LOGICAL = MODE == 2;
   constexpr int DPL = D / 16;
   // Phase A layout: G consecutive lanes share one page (lane j reads head j's
   // routing vector, so a page's G vectors are one contiguous 16*G-byte read);
   // a pass covers kPagesPerPass pages and a range kPasses passes.
   constexpr int kPagesPerPass = kDecThreads / G;
-  constexpr int kPasses = 16;
-  constexpr int kRange = kPagesPerPass * kPasses;    // 4096 / G pages
+  constexpr int kPasses = (PACKED && G >= 4) ? 32 : 16;
+  constexpr int kRange = LOGICAL ? 2048 : kPagesPerPass * kPasses;   // 4096 / G pages (8192 / G packed, G >= 4)
   constexpr int kPagesPerThread = kRange / kDecThreads;
-  __shared__ int32_t page_phys[kRange];
-  __shared__ uint8_t page_mask[kRange];
+  static_assert(!LOGICAL || kPagesPerThread == 8, "logical codes: 8 pages per thread");
+  __shared__ int32_t page_phys[LOGICAL ? 1 : kRange];
+  __shared__ uint8_t page_mask[LOGICAL ? 1 : kRange];
   __shared__ int32_t sel_phys[kRange];
   __shared__ int32_t sel_meta[kRange];
   __shared__ int32_t qroute[G][kMaxTD];
@@ -180,12 +194,61 @@ void decode_kernel(DecParams p) {
   // range's block-table entries (split 0 starts at page 0 whatever the
   // context length), the context length, the query routing vectors and Q.
   const bool prefetched = split == 0 && p.max_pages > 0;
-  int phys0[kPasses];
-  if (prefetched) {
+  int phys0[LOGICAL ? 1 : kPasses];
+  // Logical codes: block-table entries and the G heads' codes of pages
+  // lb .. lb + 7 (indices clamped to the table; results past the range are
+  // discarded).
+  auto load_logical = [&](int lb, uint32_t (&cw)[G][8], int (&ph)[8]) {
 #pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      const int l = min(ps * kPagesPerPass + pslot, p.max_pages - 1);
-      phys0[ps] = p.bt[b * p.bts0 + l * p.bts1];
+    for (int j = 0; j < 8; ++j) ph[j] = p.bt[b * p.bts0 + min(lb + j, p.max_pages - 1) * p.bts1];
+    const char* cb = static_cast<const char*>(p.lcodes);
+    if (p.lvec && lb + 8 <= p.max_pages) {
+      // 8 consecutive codes: one 8-, 16- or 32-byte read per head
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const char* src = cb + (b * p.cs0 + (h0 + g) * p.cs1 + lb) * p.code_bytes;
+        if (p.code_bytes == 1) {
+          const uint2 a = *reinterpret_cast<const uint2*>(src);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            cw[g][j] = (a.x >> (8 * j)) & 0xffu;
+            cw[g][4 + j] = (a.y >> (8 * j)) & 0xffu;
+          }
+        } else if (p.code_bytes == 2) {
+          const uint4 a = *reinterpret_cast<const uint4*>(src);
+          const uint32_t w4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) cw[g][j] = (w4[j >> 1] >> (16 * (j & 1))) & 0xffffu;
+        } else {
+          const uint4 a = reinterpret_cast<const uint4*>(src)[0], c = reinterpret_cast<const uint4*>(src)[1];
+          cw[g][0] = a.x; cw[g][1] = a.y; cw[g][2] = a.z; cw[g][3] = a.w;
+          cw[g][4] = c.x; cw[g][5] = c.y; cw[g][6] = c.z; cw[g][7] = c.w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int64_t i = b * p.cs0 + (h0 + g) * p.cs1 + min(lb + j, p.max_pages - 1) * p.cs2;
+          cw[g][j] = p.code_bytes == 1 ? static_cast<uint32_t>(reinterpret_cast<const uint8_t*>(cb)[i])
+                   : p.code_bytes == 2 ? static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(cb)[i])
+                                       : reinterpret_cast<const uint32_t*>(cb)[i];
+        }
+      }
+    }
+  };
+  uint32_t lcw0[LOGICAL ? G : 1][8];
+  int lph0[8];
+  if (prefetched) {
+    if constexpr (LOGICAL) {
+      load_logical(8 * tid, lcw0, lph0);
+    } else {
+#pragma unroll
+      for (int ps = 0; ps < kPasses; ++ps) {
+        const int l = min(ps * kPagesPerPass + pslot, p.max_pages - 1);
+        phys0[ps] = p.bt[b * p.bts0 + l * p.bts1];
+      }
     }
   }
   const int ctx = p.ctx[b];
@@ -214,13 +277,19 @@ void decode_kernel(DecParams p) {
     m_s[g] = -INFINITY;
     l_s[g] = 0.f;
   }
-  if (!p.codes) {
+  if constexpr (!PACKED) {
     for (int i = tid; i < G * p.r; i += kDecThreads) {
       const int g = i / p.r, lev = i % p.r;
       qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
     }
   }
-  const uint32_t qcode = p.codes ? p.qcodes[b * p.qcs0 + (h0 + gl) * p.qcs1] : 0u;
+  uint32_t qcode = 0u;
+  if constexpr (PACKED) qcode = p.qcodes[b * p.qcs0 + (h0 + gl) * p.qcs1];
+  uint32_t qc[LOGICAL ? G : 1];
+  if constexpr (LOGICAL) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) qc[g] = p.qcodes[b * p.qcs0 + (h0 + g) * p.qcs1];
+  }
   __syncthreads();
   int qmine[4];                 // this lane's head's first four query levels (vector path)
 #pragma unroll
@@ -234,6 +303,34 @@ void decode_kernel(DecParams p) {
     // The prefetched first range holds entries for pages past r1 as well:
     // their routing vectors are not loaded (and the pages are never selected).
     const bool use_pre = prefetched && r0 == 0;
+    const int cnt = r1 - r0;
+    int mm[kPagesPerThread];
+    int phj[LOGICAL ? 8 : 1];
+    if constexpr (LOGICAL) {
+      uint32_t cw[G][8];
+      int ph[8];
+      if (use_pre) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          ph[j] = lph0[j];
+#pragma unroll
+          for (int g = 0; g < G; ++g) cw[g][j] = lcw0[g][j];
+        }
+      } else {
+        load_logical(r0 + 8 * tid, cw, ph);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int l = r0 + 8 * tid + j;
+        const bool valid = 8 * tid + j < cnt && ph[j] >= 0 && ph[j] < p.P;
+        const bool forced = (p.sink && l == 0) || (p.local > 0 && l >= n - p.local);
+        int m = 0;
+#pragma unroll
+        for (int g = 0; g < G; ++g) m |= (((cw[g][j] ^ qc[g]) & p.code_mask) == 0u) << g;
+        mm[j] = valid ? (forced ? (1 << G) - 1 : m) : 0;
+        phj[j] = ph[j];
+      }
+    } else {
     int phys[kPasses];
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps) {
@@ -245,7 +342,7 @@ void decode_kernel(DecParams p) {
       }
     }
     bool hit[kPasses];
-    if (p.codes) {
+    if constexpr (PACKED) {
       // Packed codes: one 32-bit word per (page, head); the first r levels
       // agree iff the code bits under code_mask agree.
       uint32_t cv[kPasses];
@@ -257,7 +354,8 @@ void decode_kernel(DecParams p) {
       }
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) hit[ps] = ((cv[ps] ^ qcode) & p.code_mask) == 0u;
-    } else if (p.vec_router) {
+    } else {
+    if (p.vec_router) {
       int4 rv[kPasses];
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
@@ -290,6 +388,7 @@ void decode_kernel(DecParams p) {
         hit[ps] = ok;
       }
     }
+    }
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps) {
       const int l = r0 + ps * kPagesPerPass + pslot;
@@ -303,16 +402,16 @@ void decode_kernel(DecParams p) {
       }
     }
     __syncthreads();
-    // ---- phase A2: compact selected pages in ascending logical order -----------
-    const int cnt = r1 - r0;
-    int mm[kPagesPerThread];
-    int mine = 0;
 #pragma unroll
     for (int j = 0; j < kPagesPerThread; ++j) {
       const int l = tid * kPagesPerThread + j;
       mm[j] = l < cnt ? page_mask[l] : 0;
-      mine += mm[j] != 0;
     }
+    }
+    // ---- phase A2: compact selected pages in ascending logical order -----------
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < kPagesPerThread; ++j) mine += mm[j] != 0;
     int incl = mine;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -332,7 +431,8 @@ void decode_kernel(DecParams p) {
     for (int j = 0; j < kPagesPerThread; ++j) {
       if (mm[j] != 0) {
         const int l = tid * kPagesPerThread + j;
-        sel_phys[pos] = page_phys[l];
+        if constexpr (LOGICAL) sel_phys[pos] = phj[j];
+        else sel_phys[pos] = page_phys[l];
         sel_meta[pos] = l | (mm[j] << 16);
         ++pos;
       }
@@ -503,14 +603,21 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecParams p) {
   }
 }
 
+template <typename T, int D, int MODE>
+void launch_dp(DecParams& p, dim3 g, hipStream_t s) {
+  switch (p.G) {
+    case 1: hipLaunchKernelGGL((decode_kernel<T, D, 1, MODE>), g, dim3(kDecThreads), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<T, D, 2, MODE>), g, dim3(kDecThreads), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<T, D, 4, MODE>), g, dim3(kDecThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((decode_kernel<T, D, 8, MODE>), g, dim3(kDecThreads), 0, s, p); break;
+  }
+}
+
 template <typename T, int D>
 void launch_d(DecParams& p, dim3 g, hipStream_t s) {
-  switch (p.G) {
-    case 1: hipLaunchKernelGGL((decode_kernel<T, D, 1>), g, dim3(kDecThreads), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((decode_kernel<T, D, 2>), g, dim3(kDecThreads), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((decode_kernel<T, D, 4>), g, dim3(kDecThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((decode_kernel<T, D, 8>), g, dim3(kDecThreads), 0, s, p); break;
-  }
+  if (p.codes && p.logical) launch_dp<T, D, 2>(p, g, s);
+  else if (p.codes) launch_dp<T, D, 1>(p, g, s);
+  else launch_dp<T, D, 0>(p, g, s);
 }
 
 template <typename T>
@@ -559,7 +666,8 @@ namespace {
 // codes / qcodes (packed words, bpl bits per level, level 0 highest).
 int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
                 const int32_t* context_lens, const int32_t* router, const int32_t* q_router,
-                const uint32_t* codes, const uint32_t* qcodes, int bpl, void* out, int B, int H, int H_kv,
+                const uint32_t* codes, const uint32_t* qcodes, int bpl, int logical, void* out, int B,
+                int H, int H_kv,
                 int D, int page_size, int TD, int max_pages, int num_phys_pages, int req_depth,
                 int local_blocks, int sink_block, const int64_t* q_strides, const int64_t* k_strides,
                 const int64_t* v_strides, const int64_t* bt_strides, const int64_t* r_strides,
@@ -622,7 +730,17 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
   if (codes) {
     p.codes = codes;
     p.qcodes = qcodes;
+    p.logical = logical;
     p.cs0 = r_strides[0]; p.cs1 = r_strides[1];
+    if (logical) {
+      p.cs2 = r_strides[2];
+      p.code_bytes = logical;
+      p.lcodes = codes;
+      // 8 codes per thread with one aligned read: rows and base aligned to 8 codes
+      const int64_t al = 8 * logical >= 16 ? 16 / logical : 8;
+      p.lvec = p.cs2 == 1 && p.cs0 % al == 0 && p.cs1 % al == 0 &&
+               (reinterpret_cast<uintptr_t>(codes) % static_cast<uintptr_t>(al * logical)) == 0;
+    }
     p.qcs0 = qr_strides[0]; p.qcs1 = qr_strides[1];
     const int shift = bpl * (TD - p.r);
     p.code_mask = p.r == 0 ? 0u : (shift >= 32 ? 0u : (0xFFFFFFFFu << shift));
@@ -674,7 +792,7 @@ extern "C" int sa_sparse_paged_decode(const void* q, const void* k_cache, const 
                                       const int64_t* qr_strides, const int64_t* o_strides,
                                       void* workspace, size_t workspace_bytes, int dtype,
                                       void* stream) {
-  return sa::decode_impl(q, k_cache, v_cache, block_tables, context_lens, router, q_router, nullptr, nullptr, 0,
+  return sa::decode_impl(q, k_cache, v_cache, block_tables, context_lens, router, q_router, nullptr, nullptr, 0, 0,
                          out, B, H, H_kv, D, page_size, TD, max_pages, num_phys_pages, req_depth, local_blocks,
                          sink_block, q_strides, k_strides, v_strides, bt_strides, r_strides, qr_strides,
                          o_strides, workspace, workspace_bytes, dtype, stream);
@@ -698,8 +816,36 @@ extern "C" int sa_sparse_paged_decode_codes(const void* q, const void* k_cache, 
   }
   if (!pc_strides || !qc_strides) return fail(SA_EINVAL, "NULL strides");
   return decode_impl(q, k_cache, v_cache, block_tables, context_lens, nullptr, nullptr, page_codes, q_codes,
-                     bits_per_level, out, B, H, H_kv, D, page_size, TD, max_pages, num_phys_pages, req_depth,
+                     bits_per_level, 0, out, B, H, H_kv, D, page_size, TD, max_pages, num_phys_pages, req_depth,
                      local_blocks, sink_block, q_strides, k_strides, v_strides, bt_strides, pc_strides,
+                     qc_strides, o_strides, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int sa_sparse_paged_decode_seq_codes(const void* q, const void* k_cache, const void* v_cache,
+                                                const int32_t* block_tables, const int32_t* context_lens,
+                                                const void* seq_codes, int code_bytes, const uint32_t* q_codes,
+                                                void* out,
+                                                int B, int H, int H_kv, int D, int page_size, int TD,
+                                                int bits_per_level, int max_pages, int num_phys_pages,
+                                                int req_depth, int local_blocks, int sink_block,
+                                                const int64_t* q_strides, const int64_t* k_strides,
+                                                const int64_t* v_strides, const int64_t* bt_strides,
+                                                const int64_t* sc_strides, const int64_t* qc_strides,
+                                                const int64_t* o_strides, void* workspace,
+                                                size_t workspace_bytes, int dtype, void* stream) {
+  using namespace sa;
+  if (bits_per_level < 1 || bits_per_level > 16) return fail(SA_EINVAL, "bits_per_level must lie in [1, 16]");
+  if (TD < 1 || static_cast<long long>(TD) * bits_per_level > 32) {
+    return fail(SA_EINVAL, "tree depth x bits_per_level must be in [1, 32]");
+  }
+  if (!sc_strides || !qc_strides) return fail(SA_EINVAL, "NULL strides");
+  if (code_bytes != 1 && code_bytes != 2 && code_bytes != 4) return fail(SA_EINVAL, "code_bytes must be 1, 2 or 4");
+  if (static_cast<long long>(TD) * bits_per_level > 8 * code_bytes) {
+    return fail(SA_EINVAL, "tree depth x bits_per_level exceeds the code width");
+  }
+  return decode_impl(q, k_cache, v_cache, block_tables, context_lens, nullptr, nullptr,
+                     static_cast<const uint32_t*>(seq_codes), q_codes, bits_per_level, code_bytes, out, B, H, H_kv, D, page_size, TD, max_pages, num_phys_pages, req_depth,
+                     local_blocks, sink_block, q_strides, k_strides, v_strides, bt_strides, sc_strides,
                      qc_strides, o_strides, workspace, workspace_bytes, dtype, stream);
 }
 

@@ -20,7 +20,8 @@ from .block_list import (
     routed_block_attention,
 )
 from .kernel import block_sparse_attention, routing_to_block_indices
-from .kernel_decode import pack_routing_codes, ultrametric_decode, ultrametric_decode_packed
+from .kernel_decode import (pack_routing_codes, sequence_page_codes, ultrametric_decode,
+                            ultrametric_decode_packed, ultrametric_decode_seq_codes)
 from .surgery import RouteCache, block_list_prefill, route_block_vote
 from .ternary import pack_ternary, ternary_quantize_pack, ternary_ultrametric_attention
 
@@ -38,6 +39,8 @@ __all__ = [
     "ultrametric_decode",
     "pack_routing_codes",
     "ultrametric_decode_packed",
+    "sequence_page_codes",
+    "ultrametric_decode_seq_codes",
     "route_block_vote",
     "block_list_prefill",
     "RouteCache",

@@ -44,6 +44,9 @@ _SIGNATURES = {
     "sa_sparse_paged_decode_codes": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                           _I, _I, _I, _I, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
                                           _I64P, _P, ctypes.c_size_t, _I, _P]),
+    "sa_sparse_paged_decode_seq_codes": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                                              _I, _I, _I, _I, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
+                                              _I64P, _P, ctypes.c_size_t, _I, _P]),
     "sa_route_block_vote": (_I, [_P, _I, _I64P, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
     "sa_block_sparse_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _I, _I64P, _P, _P, _P, _P,
                                  _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _I64P, _I64P, _I64P, _I64P,

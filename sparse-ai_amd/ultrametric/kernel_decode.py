@@ -22,7 +22,8 @@ from . import _native as nat
 HAS_TRITON = nat.available()
 
 __all__ = ["HAS_TRITON", "ultrametric_decode", "_ultrametric_decode_reference", "decode_workspace_bytes",
-           "pack_routing_codes", "ultrametric_decode_packed"]
+           "pack_routing_codes", "ultrametric_decode_packed", "sequence_page_codes",
+           "ultrametric_decode_seq_codes"]
 
 
 def decode_workspace_bytes(batch_size: int, num_heads: int, head_dim: int, max_pages: int,
@@ -104,8 +105,39 @@ def ultrametric_decode_packed(q, k_cache, v_cache, block_tables, context_lens, p
                    int(bits_per_level), req_depth, local_blocks, sink_block, workspace)
 
 
+_CODE_DTYPES = {1: torch.uint8, 2: torch.int16, 4: torch.int32}
+
+
+def sequence_page_codes(page_codes: torch.Tensor, block_tables: torch.Tensor, bits: int = 32) -> torch.Tensor:
+    """(num_pages, H) page codes -> (B, H, max_pages) codes in each sequence's logical page
+    order, the layout ``ultrametric_decode_seq_codes`` reads, stored in the narrowest of
+    1 / 2 / 4 bytes that holds ``bits`` (= tree depth x bits per level). A serving cache
+    appends one column per new page instead of regathering; entries for table slots outside
+    [0, num_pages) are arbitrary (the decode never selects those pages)."""
+    width = 1 if bits <= 8 else (2 if bits <= 16 else 4)
+    idx = block_tables.long().clamp(0, page_codes.shape[0] - 1)
+    return page_codes[idx].permute(0, 2, 1).to(_CODE_DTYPES[width]).contiguous()
+
+
+def ultrametric_decode_seq_codes(q, k_cache, v_cache, block_tables, context_lens, seq_codes, q_codes,
+                                 tree_depth: int, bits_per_level: int, req_depth, local_blocks: int = 0,
+                                 sink_block: bool = False, workspace: torch.Tensor = None):
+    """``ultrametric_decode`` with routing codes stored per sequence, in logical page order:
+    seq_codes (B, H, max_pages) uint8 / int16 / int32 (bit patterns of ``pack_routing_codes``,
+    see ``sequence_page_codes``), q_codes (B, H) int32. Same output as
+    ``ultrametric_decode_packed`` on the same codes."""
+    if seq_codes.dim() != 3 or q_codes.dim() != 2:
+        raise ValueError("seq_codes must be (B, H, max_pages) and q_codes (B, H)")
+    if seq_codes.dtype not in (torch.uint8, torch.int16, torch.int32) or q_codes.dtype != torch.int32:
+        raise ValueError("seq_codes must be uint8 / int16 / int32 and q_codes int32")
+    if seq_codes.shape[2] != block_tables.shape[1]:
+        raise ValueError("seq_codes must have one column per block-table slot")
+    return _decode(q, k_cache, v_cache, block_tables, context_lens, seq_codes, q_codes, int(tree_depth),
+                   int(bits_per_level), req_depth, local_blocks, sink_block, workspace, seq=True)
+
+
 def _decode(q, k_cache, v_cache, block_tables, context_lens, rt, qrt, tree_depth, bpl, req_depth,
-            local_blocks, sink_block, workspace):
+            local_blocks, sink_block, workspace, seq=False):
     """Shared validation and launch; bpl == 0 selects the int32-level router form."""
     batch_size, num_heads, head_dim = q.shape
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
@@ -140,7 +172,10 @@ def _decode(q, k_cache, v_cache, block_tables, context_lens, rt, qrt, tree_depth
             None if workspace is None else nat.ptr(workspace), 0 if workspace is None else workspace.numel(),
             dt, nat.stream(dev))
     with torch.cuda.device(dev):
-        if bpl:
+        if bpl and seq:
+            cbytes = rt.element_size()
+            rc = lib.sa_sparse_paged_decode_seq_codes(*head[:5], head[5], cbytes, *head[6:], bpl, *tail)
+        elif bpl:
             rc = lib.sa_sparse_paged_decode_codes(*head, bpl, *tail)
         else:
             rc = lib.sa_sparse_paged_decode(*head, *tail)
