@@ -12,10 +12,11 @@ Also reported: the prefill kernel alone (HIP events around back-to-back
 launches on its stream; `roofline` is built from it), the list build alone,
 sparse paged decode on config 4 (GB/s of routed KV bytes), the backward on
 config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), the
-ternary packed-K/V prefill over config 2's lists, and a CPU baseline: the fp32 masked-dense reference (oracle) on the host cores on a
+ternary packed-K/V prefill over config 2's lists, one config-5 surgery layer
+(vote + build + prefill at N = 16384, GQA), and a CPU baseline: the fp32 masked-dense reference (oracle) on the host cores on a
 bounded sample of heads.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-backward] [--no-ternary]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-backward] [--no-ternary] [--no-c5]
 Only one GPU is supported: --gpus N > 1 exits with a message.
 """
 
@@ -59,6 +60,7 @@ def parse_args():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward measurement")
     ap.add_argument("--no-ternary", action="store_true", help="skip the ternary packed-K/V measurement")
+    ap.add_argument("--no-c5", action="store_true", help="skip the config-5 surgery-layer measurement")
     ap.add_argument("--cpu-heads", type=int, default=32, help="heads timed for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU work for the CPU baseline (whole passes over --cpu-heads)")
@@ -335,6 +337,39 @@ def main():
         }
         log(f"ternary prefill {tern_ms * 1e3:.1f} us, {flop_alg / (tern_ms * 1e-3) / 1e12:.0f} TFLOP/s")
         del qh, kp, vp, ksc, vsc, tout
+
+    # ---------------- config 5: one surgery layer (vote + sync-free build + prefill) -----
+    if not args.no_c5:
+        from ultrametric import block_list_prefill
+        g5 = torch.Generator(device="cpu").manual_seed(5)
+        S5, H5, Hkv5, L5, p5, r5 = 16384, 32, 8, 4, 4, 2
+        q5 = torch.randn(1, H5, S5, D, generator=g5).to(torch.bfloat16).to(dev)
+        k5 = torch.randn(1, Hkv5, S5, D, generator=g5).to(torch.bfloat16).to(dev)
+        v5 = torch.randn(1, Hkv5, S5, D, generator=g5).to(torch.bfloat16).to(dev)
+        a5 = torch.randn(1, H5, S5, L5, p5, generator=g5).to(dev)
+
+        def layer():
+            return block_list_prefill(q5, k5, v5, a5, r5, p=p5, route_block=RB, local_window=16)
+
+        with torch.no_grad():
+            for _ in range(3):
+                layer()
+            c5_ms = time_launches(layer, 20, torch)
+            _, st5 = block_list_prefill(q5, k5, v5, a5, r5, p=p5, route_block=RB, local_window=16,
+                                        return_stats=True)
+        tiles5 = st5["block_density"] * H5 * (S5 // RB) * (S5 // RB + 1) / 2
+        flop5 = 4 * D * RB * RB * tiles5
+        result["surgery_layer_c5"] = {
+            "workload": "config5 layer: Llama-3.1-8B shape, N 16384, 32 q / 8 kv heads (GQA native), D 128, "
+                        "route block 128, p 4, 4 levels, r 2, sink + 1 local block; per-token scores voted "
+                        "per block, sync-free lists, prefill; bf16",
+            "ms_per_layer": round(c5_ms, 5),
+            "block_density_causal": round(st5["block_density"], 4),
+            "tflops_computed_tiles": round(flop5 / (c5_ms * 1e-3) / 1e12, 1),
+            "ms_32_layers": round(32 * c5_ms, 4),
+        }
+        log(f"surgery layer (config 5) {c5_ms * 1e3:.1f} us, density {st5['block_density']:.3f}")
+        del q5, k5, v5, a5
 
     # ---------------- config 3: density sweep (optional) ------------------------------
     if args.sweep:

@@ -112,3 +112,29 @@ def test_route_cache_reuses_anchor_lists():
     # a different routing depth is a different key: layer 3 routes by itself
     got = block_list_prefill(q, k, v, a0, 1, route_cache=cache, layer_idx=3, **kw)
     assert torch.equal(got, block_list_prefill(q, k, v, a0, 1, **kw))
+
+
+def test_block_list_prefill_config5_layer():
+    # config 5: one Llama-3.1-8B layer at N = 16384 (32 query / 8 kv heads, D 128,
+    # route block 128, p = 4, 4 levels, r = 2, local window 16 -> 1 block, sink)
+    g = torch.Generator().manual_seed(55)
+    B, H, Hkv, S, D, L, p, rb, r = 1, 32, 8, 16384, 128, 4, 4, 128, 2
+    q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    a = torch.randn(B, H, S, L, p, generator=g)
+    out, st = block_list_prefill(q.to(DEV), k.to(DEV), v.to(DEV), a.to(DEV), r, p=p, route_block=rb,
+                                 local_window=16, return_stats=True)
+    route = osg.majority_route(a.numpy(), r, rb)
+    bl = ob.build_block_lists(route, r, is_causal=True, sink_block=True, local_blocks=1, arity=p)
+    mask = ob.lists_to_mask(bl.lists, bl.counts)
+    heads = [(0, 0), (0, 13), (0, 31)]
+    kk = np.repeat(k.float().numpy(), H // Hkv, axis=1)
+    vv = np.repeat(v.float().numpy(), H // Hkv, axis=1)
+    ref, _ = oa.block_sparse_attention_ref(q.float().numpy(), kk, vv, mask, rb, is_causal=True, heads=heads)
+    got = out.float().cpu().numpy()
+    for z, h in heads:
+        assert np.abs(got[z, h] - ref[z, h]).max() <= 2e-2, h
+    assert torch.isfinite(out).all()
+    # SURVEY: about 763 of 8256 causal blocks per head at r = 2 (9.2%)
+    assert 0.05 < st["block_density"] < 0.15
