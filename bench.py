@@ -419,7 +419,7 @@ def main():
             "routed_kv_bytes": b_alg, "unique_pages": upages,
             "routing_metadata_bytes": meta_bytes,
             "gbs_routed": round(dec_gbs, 1),
-            "roofline": {"kernel": "decode_kernel<bf16, D=128, G=4>", "bound": "hbm", "achieved": round(dec_gbs, 1),
+            "roofline": {"kernel": "decode_kernel<bf16, D=128, G=4, mode 0 (reference router)>", "bound": "hbm", "achieved": round(dec_gbs, 1),
                          "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(dec_gbs / PEAK_HBM_GBS, 4),
                          "traffic": profiled_traffic("decode_config4_bf16.md"),
                          "traffic_source": "profiles/decode_config4_bf16.md"},
