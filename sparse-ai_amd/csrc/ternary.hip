@@ -329,6 +329,79 @@ __global__ __launch_bounds__(256) void ternary_pack_kernel(const T* x, int64_t x
   if (lane == 0 && scale) scale[r] = gamma;
 }
 
+// Rows with D / 16 a power of two <= 64 and unit element stride: lane j of
+// the LPR lanes of a row owns word j (16 consecutive values, loaded as
+// vectors); gamma is reduced over the row's lanes with shuffles.
+template <typename T, int LPR>
+__global__ __launch_bounds__(256) void ternary_pack_rows_kernel(const T* x, int64_t xs0, int rows, int mode,
+                                                                int32_t* packed, float* scale) {
+  constexpr int D = 16 * LPR;
+  const int tid = blockIdx.x * 256 + threadIdx.x;
+  const int r = tid / LPR, w = tid % LPR;
+  const bool ok = r < rows;
+  const T* xr = x + static_cast<int64_t>(ok ? r : 0) * xs0 + 16 * w;
+  float v[16];
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 f = reinterpret_cast<const float4*>(xr)[i];
+      v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 u = reinterpret_cast<const uint4*>(xr)[i];
+      const uint32_t ww[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if constexpr (std::is_same<T, bf16_t>::value) {
+          v[8 * i + 2 * e] = bf16_bits_to_float(ww[e] & 0xffffu);
+          v[8 * i + 2 * e + 1] = bf16_bits_to_float(ww[e] >> 16);
+        } else {
+          v[8 * i + 2 * e] = f16_bits_to_float(ww[e] & 0xffffu);
+          v[8 * i + 2 * e + 1] = f16_bits_to_float(ww[e] >> 16);
+        }
+      }
+    }
+  }
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) a += fabsf(v[i]);
+#pragma unroll
+  for (int o = 1; o < LPR; o <<= 1) a += __shfl_xor(a, o);
+  const float gamma = mode == 0 ? a / static_cast<float>(D) : 1.f;
+  const float thr = 0.5f * gamma;
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t c = mode == 0 ? (v[i] > thr ? 1u : (v[i] < -thr ? 2u : 0u))
+                                 : (v[i] == 1.f ? 1u : (v[i] == -1.f ? 2u : 0u));
+    word |= c << (2 * i);
+  }
+  if (ok) {
+    packed[static_cast<int64_t>(r) * LPR + w] = static_cast<int32_t>(word);
+    if (w == 0 && scale) scale[r] = gamma;
+  }
+}
+
+template <typename T>
+int launch_pack_rows(const T* x, int64_t xs0, int rows, int D, int mode, int32_t* packed, float* scale,
+                     hipStream_t s) {
+  const int lpr = D / 16;
+  const long long threads = static_cast<long long>(rows) * lpr;
+  const unsigned g = static_cast<unsigned>((threads + 255) / 256);
+  switch (lpr) {
+    case 1: hipLaunchKernelGGL((ternary_pack_rows_kernel<T, 1>), dim3(g), dim3(256), 0, s, x, xs0, rows, mode, packed, scale); break;
+    case 2: hipLaunchKernelGGL((ternary_pack_rows_kernel<T, 2>), dim3(g), dim3(256), 0, s, x, xs0, rows, mode, packed, scale); break;
+    case 4: hipLaunchKernelGGL((ternary_pack_rows_kernel<T, 4>), dim3(g), dim3(256), 0, s, x, xs0, rows, mode, packed, scale); break;
+    case 8: hipLaunchKernelGGL((ternary_pack_rows_kernel<T, 8>), dim3(g), dim3(256), 0, s, x, xs0, rows, mode, packed, scale); break;
+    case 16: hipLaunchKernelGGL((ternary_pack_rows_kernel<T, 16>), dim3(g), dim3(256), 0, s, x, xs0, rows, mode, packed, scale); break;
+    case 32: hipLaunchKernelGGL((ternary_pack_rows_kernel<T, 32>), dim3(g), dim3(256), 0, s, x, xs0, rows, mode, packed, scale); break;
+    default: hipLaunchKernelGGL((ternary_pack_rows_kernel<T, 64>), dim3(g), dim3(256), 0, s, x, xs0, rows, mode, packed, scale); break;
+  }
+  return check_launch("ternary pack kernel");
+}
+
 }  // namespace
 }  // namespace sa
 
@@ -342,8 +415,17 @@ extern "C" int sa_ternary_pack(const void* x, int dtype, const int64_t* strides,
   }
   if (rows == 0) return SA_OK;
   if (!x || !strides || !packed) return fail(SA_EINVAL, "NULL argument");
-  const unsigned g = static_cast<unsigned>((static_cast<long long>(rows) + 3) / 4);
   hipStream_t s = as_stream(stream);
+  // Vector path: D / 16 a power of two <= 64, unit element stride, 16-byte aligned rows.
+  const int lpr = D / 16;
+  const int64_t esz = dtype == SA_DTYPE_F32 ? 4 : 2;
+  if ((lpr & (lpr - 1)) == 0 && lpr <= 64 && strides[1] == 1 && (strides[0] * esz) % 16 == 0 &&
+      (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && static_cast<long long>(rows) * lpr < (1LL << 31)) {
+    if (dtype == SA_DTYPE_F32) return launch_pack_rows(static_cast<const float*>(x), strides[0], rows, D, mode, packed, scale, s);
+    if (dtype == SA_DTYPE_BF16) return launch_pack_rows(static_cast<const bf16_t*>(x), strides[0], rows, D, mode, packed, scale, s);
+    return launch_pack_rows(static_cast<const f16_t*>(x), strides[0], rows, D, mode, packed, scale, s);
+  }
+  const unsigned g = static_cast<unsigned>((static_cast<long long>(rows) + 3) / 4);
   if (dtype == SA_DTYPE_F32)
     hipLaunchKernelGGL((ternary_pack_kernel<float>), dim3(g), dim3(256), 0, s, static_cast<const float*>(x),
                        strides[0], strides[1], rows, D, mode, packed, scale);
