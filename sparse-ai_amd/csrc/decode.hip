@@ -140,11 +140,6 @@ __device__ __forceinline__ float row_dot(const uint32_t* a, const RowRegs<T, DPL
   return s;
 }
 
-__device__ __forceinline__ uint32_t lanes_below(uint64_t ballot) {
-  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ballot >> 32),
-                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ballot), 0u));
-}
-
 // MODE 0: int32 routing levels per (physical page, head) (the reference's
 // router). MODE 1: packed routing codes per (physical page, head); the
 // phase-A registers are then small enough for 2048-page ranges at G >= 4.
