@@ -136,9 +136,9 @@ int launch(BLParams& p, int mode, int id_dtype, hipStream_t stream) {
     return fail(SA_EUNSUPPORTED, "block-list builder supports NB <= 8192, got " + std::to_string(p.NB));
   }
   if (p.lists && p.cols < 0) return fail(SA_EINVAL, "lists_cols must be >= 0");
-  if (!p.counts) return fail(SA_EINVAL, "counts must not be NULL");
   const long long rows_total = static_cast<long long>(p.Z) * p.H * p.NB;
-  if (rows_total == 0) return SA_OK;
+  if (rows_total == 0) return SA_OK;                     // empty tensors may carry NULL
+  if (!p.counts) return fail(SA_EINVAL, "counts must not be NULL");
   // Rows per wave: as few as keeps ~kTargetWaves waves busy (each workgroup
   // recomputes its head's NB codes, a cached read of NB * TD ids).
   long long rpw = (rows_total + kTargetWaves - 1) / kTargetWaves;
@@ -183,7 +183,9 @@ extern "C" int sa_build_block_lists(const void* router, int router_dtype,
     return fail(SA_EINVAL, "req_depth out of range [0, TD]");
   }
   if (use_codes && base < 2) return fail(SA_EINVAL, "code base must be >= 2");
-  if (!router || !router_strides) return fail(SA_EINVAL, "router must not be NULL");
+  if (!router_strides || (!router && static_cast<long long>(Z) * H * NB > 0)) {
+    return fail(SA_EINVAL, "router must not be NULL");
+  }
   BLParams p{};
   p.router = router;
   p.rs0 = router_strides[0];
@@ -211,7 +213,9 @@ extern "C" int sa_build_block_lists_mask(const uint8_t* mask, const int64_t* mas
                                          int local_blocks, int32_t* lists, int lists_cols,
                                          int32_t* counts, void* stream) {
   using namespace sa;
-  if (!mask || !mask_strides) return fail(SA_EINVAL, "mask must not be NULL");
+  if (!mask_strides || (!mask && static_cast<long long>(Z) * H * NB > 0)) {
+    return fail(SA_EINVAL, "mask must not be NULL");
+  }
   BLParams p{};
   p.mask = mask;
   p.ms0 = mask_strides[0];

@@ -565,9 +565,6 @@ extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, 
                                    const int64_t* sb_strides, float sm_scale, int dtype,
                                    int is_causal, void* stream) {
   using namespace sa;
-  if (!q || !k || !v || !out || !counts || (!lists && max_count > 0)) {
-    return fail(SA_EINVAL, "NULL tensor argument");
-  }
   if (!q_strides || !k_strides || !v_strides || !o_strides) return fail(SA_EINVAL, "NULL strides");
   if (Z < 0 || H < 0 || N < 0 || H_kv <= 0 || (H > 0 && H % H_kv != 0)) {
     return fail(SA_EINVAL, "bad Z/H/H_kv/N");
@@ -586,7 +583,10 @@ extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, 
     return fail(SA_EINVAL, "soft_bias needs strides and an f32/bf16/f16 dtype");
   }
   if (max_count < 0) return fail(SA_EINVAL, "max_count must be >= 0");
-  if (static_cast<long long>(Z) * H * N == 0) return SA_OK;
+  if (static_cast<long long>(Z) * H * N == 0) return SA_OK;    // empty tensors may carry NULL
+  if (!q || !k || !v || !out || !counts || (!lists && max_count > 0)) {
+    return fail(SA_EINVAL, "NULL tensor argument");
+  }
 
   FwdParams p{};
   p.q = q; p.k = k; p.v = v; p.out = out; p.lse = lse;

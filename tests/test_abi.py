@@ -133,3 +133,25 @@ def test_python_validation_matches_reference_errors():
         block_list_attention(q, q, q, bl, route_block=32)
     with pytest.raises(ValueError, match="divide"):
         block_list_attention(q, q, q, bl, route_block=64, block_m=48)
+
+
+def test_empty_problems_accept_null_data():
+    # zero-size tensors hand over NULL data pointers; an empty problem is a
+    # no-op (no launch, no device call) whatever the pointers
+    lib = nat.lib()
+    s = [(ctypes.c_int64 * 5)(1, 1, 1, 1, 1) for _ in range(8)]
+    N0 = None
+    assert lib.sa_build_block_lists(N0, 3, s[0], 0, 2, 4, 2, None, 1, 2, 1, 1, 0, 0, N0, 4, N0, None) == nat.SA_OK
+    assert lib.sa_build_block_lists_mask(N0, s[0], 1, 0, 4, 1, 0, 0, N0, 4, N0, None) == nat.SA_OK
+    assert lib.sa_transpose_block_lists(N0, N0, 4, 0, 2, 4, N0, 4, N0, None) == nat.SA_OK
+    for Z, H, N in ((0, 2, 64), (1, 0, 64), (1, 2, 0)):
+        assert lib.sa_block_sparse_fwd(N0, N0, N0, N0, N0, N0, N0, N0, 0, Z, H, 1 if H == 0 else H, N, 64, 64, 1,
+                                       s[0], s[1], s[2], s[3], None, 0.1, 1, 1, None) == nat.SA_OK, (Z, H, N)
+    assert lib.sa_route_block_vote(N0, 0, s[0], 0, 2, 64, 3, 2, 1, 32, N0, None) == nat.SA_OK
+    assert lib.sa_pack_page_codes(N0, s[0], 0, 4, 3, 2, N0, None) == nat.SA_OK
+    assert lib.sa_ternary_pack(N0, 1, s[0], 0, 64, 0, N0, N0, None) == nat.SA_OK
+    assert lib.sa_ternary_prefill_fwd(N0, N0, N0, N0, N0, 0, N0, N0, 1, N0, 0, 2, 2, 256, 64, 0,
+                                      *s[:6], None) == nat.SA_OK
+    dec = [N0] * 8 + [0, 8, 2, 64, 16, 3, 2, 4, 2, 0, 0] + s[:7] + [N0, 0, 1, None]
+    assert lib.sa_sparse_paged_decode(*dec) == nat.SA_OK
+    assert lib.sa_block_sparse_bwd_plan_bytes(0, 2, 2, 64, 64, 1) == 0
