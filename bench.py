@@ -56,6 +56,9 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--spinup-ms", type=float, default=200.0,
+                    help="untimed steps run back to back for this long before the warmup steps, so that "
+                         "the timed steps run at the GPU's steady clocks")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward measurement")
@@ -98,6 +101,20 @@ def time_launches(fn, reps, torch):
     e.record()
     torch.cuda.synchronize()
     return s.elapsed_time(e) / reps
+
+
+def spin_up(fn, ms, torch):
+    """Calls `fn` back to back for `ms` milliseconds (untimed), then synchronizes: the
+    first tens of milliseconds of continuous work run below the GPU's steady clocks
+    (the config-2 step measured 90.6 then 80.9 us in two consecutive 200-step blocks).
+    Returns the number of calls."""
+    n = 0
+    end = time.perf_counter() + ms * 1e-3
+    while time.perf_counter() < end:
+        fn()
+        n += 1
+    torch.cuda.synchronize()
+    return n
 
 
 def density_sweep(torch, wl, nat, dev, reps):
@@ -201,7 +218,8 @@ def main():
         return block_list_attention(q, k, v, b, route_block=RB, is_causal=True)
 
     with torch.no_grad():
-        log(f"warmup {args.warmup}")
+        spin_steps = spin_up(step, args.spinup_ms, torch)   # untimed, before the warmup steps
+        log(f"spin-up {spin_steps} steps, warmup {args.warmup}")
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
@@ -246,6 +264,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "spinup_steps": spin_steps,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -404,6 +423,7 @@ def main():
             nat.check(dec_fn(*dargs))
 
         with torch.no_grad():
+            spin_up(dec, args.spinup_ms, torch)   # the GPU idled while config 4 was generated
             for _ in range(args.warmup):
                 dec()
             dec_ms = time_launches(dec, max(50, args.steps), torch)
