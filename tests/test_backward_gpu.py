@@ -191,3 +191,20 @@ def test_backward_mfma_soft_bias_ste(causal):
     assert np.abs(got - want).max() <= 2e-2 * max(1.0, np.abs(want).max())
     check_grads((q.grad.float().cpu().numpy(), k.grad.float().cpu().numpy(), v.grad.float().cpu().numpy()),
                 ref[:3])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_backward_expanded_output_gradient(dtype):
+    # out.sum() hands the backward an expanded gradient (every stride 0): the
+    # same gradients as an explicit, contiguous all-ones gradient
+    torch.manual_seed(11)
+    Z, H, N, D, rb = 1, 2, 320, 64, 64
+    q0, k0, v0 = (torch.randn(Z, H, N, D).to(dtype) for _ in range(3))
+    router = random_router(Z, H, N // rb, 3, 2, seed=5).to(DEV)
+    bl = build_block_lists(router, 1, is_causal=True, sink_block=True, arity=2)
+    q, k, v = (t.to(DEV).clone().requires_grad_(True) for t in (q0, k0, v0))
+    block_list_attention(q, k, v, bl, route_block=rb, is_causal=True).sum().backward()
+    got = (q.grad.float().cpu().numpy(), k.grad.float().cpu().numpy(), v.grad.float().cpu().numpy())
+    ones = torch.ones(Z, H, N, D).to(dtype)
+    ref = oracle(q0, k0, v0, ones, bl, rb, True)
+    check_grads(got, ref[:3], rel=2e-2 if dtype == torch.bfloat16 else 1e-4)
