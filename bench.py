@@ -13,10 +13,14 @@ launches on its stream; `roofline` is built from it), the list build alone,
 sparse paged decode on config 4 (GB/s of routed KV bytes), the backward on
 config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), the
 ternary packed-K/V prefill over config 2's lists, one config-5 surgery layer
-(vote + build + prefill at N = 16384, GQA), and a CPU baseline: the fp32 masked-dense reference (oracle) on the host cores on a
-bounded sample of heads.
+(vote + build + prefill at N = 16384, GQA), and CPU baselines on the host
+cores: the fp32 masked-dense reference (oracle) on a bounded sample of config
+2's heads, and the float64 decode oracle on the first sequences of config 4.
+Untimed steps run back to back for --spinup-ms before the warmup steps, so
+that the timed steps run at the GPU's steady clocks.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-backward] [--no-ternary] [--no-c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup-ms MS] [--no-cpu] [--no-decode]
+                       [--no-backward] [--no-ternary] [--no-c5]
 Only one GPU is supported: --gpus N > 1 exits with a message.
 """
 
@@ -499,6 +503,45 @@ def main():
             "layout": f"(B, H, max_pages) {8 * sc.element_size()}-bit codes in logical page order, read with the block table",
         }
         log(f"decode (sequence codes) {sdec_ms * 1e3:.1f} us/call, {sgbs:.0f} GB/s on routed bytes")
+
+        if not args.no_cpu:
+            # decode: the float64 loop oracle (the reference's _ultrametric_decode_reference
+            # semantics, GQA grouped) over the first sequences of config 4, with only their
+            # pages copied to the host
+            import numpy as np
+            from oracle import decode as od
+            ns = min(4, B)
+            ctx_s = w.context_lens[:ns].cpu().numpy().astype(np.int64)
+            npg = (ctx_s + PS - 1) // PS
+            bt_s = w.block_tables[:ns].cpu().numpy().astype(np.int64)
+            used = np.unique(np.concatenate([bt_s[i, :npg[i]] for i in range(ns)]))
+            bt_c = np.zeros_like(bt_s)
+            for i in range(ns):
+                bt_c[i, :npg[i]] = np.searchsorted(used, bt_s[i, :npg[i]])
+            used_t = torch.from_numpy(used).to(dev)
+            kc_s = w.k_cache[used_t].float().cpu().numpy()
+            vc_s = w.v_cache[used_t].float().cpu().numpy()
+            r_s = w.router[used_t].cpu().numpy()
+            q_s = w.q[:ns].float().cpu().numpy()
+            qr_s = w.q_router[:ns].cpu().numpy()
+            od.decode_reference(q_s[:1], kc_s, vc_s, bt_c[:1], ctx_s[:1], r_s, qr_s[:1], **kw)
+            dpasses, t0 = 0, time.perf_counter()
+            while True:
+                od.decode_reference(q_s, kc_s, vc_s, bt_c, ctx_s, r_s, qr_s, **kw)
+                dpasses += 1
+                if time.perf_counter() - t0 >= min(args.cpu_seconds, 5.0):
+                    break
+            dcpu_s = (time.perf_counter() - t0) / dpasses
+            b_s, _ = od.routed_page_bytes(bt_c, ctx_s, r_s, qr_s, Hkv, PS, Dd, 2, **kw)
+            result["decode"]["cpu_baseline"] = {
+                "value": round(b_s / dcpu_s / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+                "kind": "port",
+                "sample": f"float64 decode oracle (oracle/decode.py decode_reference, the reference's "
+                          f"_ultrametric_decode_reference loop) on the first {ns} of {B} sequences, all "
+                          f"{Hq} heads; {dpasses} passes, {dcpu_s * 1e3:.1f} ms per pass; value = routed "
+                          f"bytes of those sequences / wall time per pass",
+            }
+            log(f"decode cpu baseline {dcpu_s * 1e3:.1f} ms per pass over {ns} sequences")
         del w
 
     # ---------------- CPU baseline (oracle, host cores) --------------------------------
