@@ -29,6 +29,7 @@ implemented here yet; a forward that needs grad raises RuntimeError.
 
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import NamedTuple, Optional, Sequence, Union
 
@@ -407,6 +408,20 @@ def block_list_attention(
 # Backward
 # ----------------------------------------------------------------------------
 
+_SIDE_STREAMS = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for backward work that does not
+    feed dQ."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get(idx)
+    if st is None:
+        st = torch.cuda.Stream(device=idx)
+        _SIDE_STREAMS[idx] = st
+    return st
+
+
 def _launch_bwd(dout, q, k, v, out, lse, lists, counts, max_count, soft_block_bias, route_block,
                 is_causal, scale):
     """dq, dk, dv (and the soft-bias gradient) of block-list attention
@@ -419,23 +434,51 @@ def _launch_bwd(dout, q, k, v, out, lse, lists, counts, max_count, soft_block_bi
     dt = nat.dtype_code(q.dtype, (torch.float32, torch.bfloat16, torch.float16))
     if dout.dtype != q.dtype:
         dout = dout.to(q.dtype)
-    t_lists, t_counts, t_max = _transposed_lists_sync_free(lists, counts, max_count, nb)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
-    delta = torch.empty((Z, H, N), dtype=torch.float32, device=dev)
     sb = soft_block_bias
     sb_code = 0
-    dsb = None
     if sb is not None:
         if sb.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             sb = sb.float()
         sb_code = nat.DTYPE_CODES[sb.dtype]
-        dsb = torch.zeros((Z, H, nb, max_count), dtype=torch.float32, device=dev)
+    sb_st = nat.strides(sb) if sb is not None else None
     lib = nat.lib()
     lists_p = nat.ptr(lists) if max_count > 0 else None
-    t_lists_p = nat.ptr(t_lists) if t_max > 0 else None
-    sb_st = nat.strides(sb) if sb is not None else None
+    mfma = not (q.dtype == torch.float32 or route_block < 32 or Z * H * N == 0)
+
+    # MFMA path: the transposed lists and the dK/dV work plan do not feed dQ, so they
+    # are built on a second stream while dQ runs on the caller's stream, which waits
+    # for them before dK/dV. The plan's item counts are the backward's one host read
+    # (the reference reads max(q_counts) at this point, block_list.py:320).
+    main = torch.cuda.current_stream(dev)
+    if mfma:
+        side = _side_stream(dev)
+        side.wait_stream(main)
+        where = torch.cuda.stream(side)
+    else:
+        where = contextlib.nullcontext()
+    with where:
+        t_lists, t_counts, t_max = _transposed_lists_sync_free(lists, counts, max_count, nb)
+        t_lists_p = nat.ptr(t_lists) if t_max > 0 else None
+        if mfma:
+            nbytes = int(lib.sa_block_sparse_bwd_plan_bytes(Z, H, Hkv, N, int(route_block), int(t_max)))
+            plan = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            info = torch.empty(3, dtype=torch.int32, device=dev)
+            with torch.cuda.device(dev):
+                rc = lib.sa_block_sparse_bwd_plan(lists_p, nat.ptr(counts), int(max_count), t_lists_p,
+                                                  nat.ptr(t_counts), int(t_max), nat.ptr(sb), sb_code, sb_st, Z, H,
+                                                  Hkv, N, int(route_block), nat.ptr(plan), nbytes, nat.ptr(info),
+                                                  nat.stream(dev))
+            nat.check(rc)
+            info_host = torch.empty(3, dtype=torch.int32, pin_memory=True)
+            info_host.copy_(info, non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record(side)
+
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    delta = torch.empty((Z, H, N), dtype=torch.float32, device=dev)
+    dsb = torch.zeros((Z, H, nb, max_count), dtype=torch.float32, device=dev) if sb is not None else None
 
     def launch(phases, plan=None, n_work=0, n_multi=0, partials=None):
         with torch.cuda.device(dev):
@@ -451,26 +494,13 @@ def _launch_bwd(dout, q, k, v, out, lse, lists, counts, max_count, soft_block_bi
                 nat.stream(dev))
         nat.check(rc)
 
-    if q.dtype == torch.float32 or route_block < 32 or Z * H * N == 0:
+    if not mfma:
         launch(3)
         return dq, dk, dv, dsb
-    # Work plan of the MFMA dK/dV kernels. Its item counts are the backward's one
-    # host read (the reference reads max(q_counts) at this point, block_list.py:320);
-    # the dQ phase is queued before the read, so the GPU keeps working meanwhile.
-    nbytes = int(lib.sa_block_sparse_bwd_plan_bytes(Z, H, Hkv, N, int(route_block), int(t_max)))
-    plan = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    info = torch.empty(3, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
-        rc = lib.sa_block_sparse_bwd_plan(lists_p, nat.ptr(counts), int(max_count), t_lists_p, nat.ptr(t_counts),
-                                          int(t_max), nat.ptr(sb), sb_code, sb_st, Z, H, Hkv, N,
-                                          int(route_block), nat.ptr(plan), nbytes, nat.ptr(info), nat.stream(dev))
-    nat.check(rc)
-    info_host = torch.empty(3, dtype=torch.int32, pin_memory=True)
-    with torch.cuda.device(dev):
-        info_host.copy_(info, non_blocking=True)
-        ready = torch.cuda.Event()
-        ready.record()
-    launch(1)
+    launch(1)                       # dQ (with delta) reads only the forward lists
+    main.wait_stream(side)
+    for t in (t_lists, t_counts, plan):
+        t.record_stream(main)
     ready.synchronize()
     n_work, n_multi, n_multi_items = info_host.tolist()
     partials = None
