@@ -194,8 +194,17 @@ void decode_kernel(DecParams p) {
   // lb .. lb + 7 (indices clamped to the table; results past the range are
   // discarded).
   auto load_logical = [&](int lb, uint32_t (&cw)[G][8], int (&ph)[8]) {
+    if (p.bts1 == 1 && (p.bts0 & 3) == 0 && (reinterpret_cast<uintptr_t>(p.bt) & 15) == 0 &&
+        lb + 8 <= p.max_pages) {
+      // 8 consecutive entries, 16-byte aligned: two 16-byte reads
+      const int4* src = reinterpret_cast<const int4*>(p.bt + static_cast<int64_t>(b) * p.bts0 + lb);
+      const int4 u0 = src[0], u1 = src[1];
+      ph[0] = u0.x; ph[1] = u0.y; ph[2] = u0.z; ph[3] = u0.w;
+      ph[4] = u1.x; ph[5] = u1.y; ph[6] = u1.z; ph[7] = u1.w;
+    } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ph[j] = p.bt[b * p.bts0 + min(lb + j, p.max_pages - 1) * p.bts1];
+      for (int j = 0; j < 8; ++j) ph[j] = p.bt[b * p.bts0 + min(lb + j, p.max_pages - 1) * p.bts1];
+    }
     const char* cb = static_cast<const char*>(p.lcodes);
     if (p.lvec && lb + 8 <= p.max_pages) {
       // 8 consecutive codes: one 8-, 16- or 32-byte read per head
@@ -256,23 +265,36 @@ void decode_kernel(DecParams p) {
   const int grp = lane >> 4, sub = lane & 15;
   constexpr int QW = RowRegs<T, DPL>::kWords;
   uint32_t qw[G][QW];  // this lane's D/16 query elements per head, raw
+  // One vector read per head when the lane's D/16 elements are contiguous and aligned.
+  constexpr int kQBytes = DPL * static_cast<int>(sizeof(T));
+  constexpr int kQAlign = kQBytes >= 16 ? 16 : kQBytes;
+  const bool qvec = p.qs2 == 1 && ((p.qs0 | p.qs1) * static_cast<int64_t>(sizeof(T))) % kQAlign == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.q) % kQAlign) == 0;
   float m_s[G], l_s[G], acc[G][DPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const T* qp = static_cast<const T*>(p.q) + b * p.qs0 + (h0 + g) * p.qs1 + sub * DPL * p.qs2;
 #pragma unroll
     for (int i = 0; i < QW; ++i) qw[g][i] = 0u;
+    if (qvec) {
+      RowRegs<T, DPL> qr;
+      load_row<T, DPL>(qp, qr);
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) {
-      const uint32_t bits = elem_bits<T>(qp + e * p.qs2);
-      if constexpr (sizeof(T) == 4) qw[g][e] = bits;
-      else qw[g][e >> 1] |= bits << (16 * (e & 1));
-      acc[g][e] = 0.f;
+      for (int i = 0; i < QW; ++i) qw[g][i] = qr.w[i];
+    } else {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const uint32_t bits = elem_bits<T>(qp + e * p.qs2);
+        if constexpr (sizeof(T) == 4) qw[g][e] = bits;
+        else qw[g][e >> 1] |= bits << (16 * (e & 1));
+      }
     }
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
     m_s[g] = -INFINITY;
     l_s[g] = 0.f;
   }
-  if constexpr (!PACKED) {
+  if constexpr (!PACKED && !LOGICAL) {   // the code modes carry no level-wise query router
     for (int i = tid; i < G * p.r; i += kDecThreads) {
       const int g = i / p.r, lev = i % p.r;
       qroute[g][lev] = p.qr[b * p.qrs0 + (h0 + g) * p.qrs1 + lev * p.qrs2];
@@ -286,9 +308,11 @@ void decode_kernel(DecParams p) {
     for (int g = 0; g < G; ++g) qc[g] = p.qcodes[b * p.qcs0 + (h0 + g) * p.qcs1];
   }
   __syncthreads();
-  int qmine[4];                 // this lane's head's first four query levels (vector path)
+  int qmine[4] = {0, 0, 0, 0};  // this lane's head's first four query levels (vector path)
+  if constexpr (!PACKED && !LOGICAL) {
 #pragma unroll
-  for (int lev = 0; lev < 4; ++lev) qmine[lev] = lev < p.r ? qroute[gl][lev] : 0;
+    for (int lev = 0; lev < 4; ++lev) qmine[lev] = lev < p.r ? qroute[gl][lev] : 0;
+  }
 
   for (int r0 = pa; r0 < pz; r0 += kRange) {
     const int r1 = min(pz, r0 + kRange);
