@@ -27,6 +27,7 @@ sys.path.insert(0, ROOT)
 from oracle import attention as oa  # noqa: E402
 from oracle import blocks as ob  # noqa: E402
 from oracle import decode as od  # noqa: E402
+from oracle import ternary as ot  # noqa: E402
 
 
 def bf16_round(x):
@@ -116,10 +117,54 @@ def make_decode(path):
     np.savez_compressed(path, **out)
 
 
+def make_backward(path):
+    # bf16 inputs on the MFMA backward's shapes: GQA 4/2, route block 64, causal with sink
+    rng = np.random.default_rng(4004)
+    Z, H, Hkv, N, D, RB = 1, 4, 2, 256, 64, 64
+    NB = N // RB
+    qb, qf = bf16_round(rng.standard_normal((Z, H, N, D)).astype(np.float32))
+    kb, kf = bf16_round(rng.standard_normal((Z, Hkv, N, D)).astype(np.float32))
+    vb, vf = bf16_round(rng.standard_normal((Z, Hkv, N, D)).astype(np.float32))
+    gb, gf = bf16_round(rng.standard_normal((Z, H, N, D)).astype(np.float32))
+    router = rng.integers(0, 2, size=(Z, H, NB, 2), dtype=np.int32)
+    bl = ob.build_block_lists(router, 1, is_causal=True, sink_block=True, arity=2)
+    mask = ob.lists_to_mask(bl.lists, bl.counts)
+    dq, dk, dv, _ = oa.block_sparse_attention_grad_ref(qf, kf, vf, mask, RB, gf, is_causal=True)
+    np.savez_compressed(path, q_bits=qb, k_bits=kb, v_bits=vb, do_bits=gb, lists=bl.lists.astype(np.int32),
+                        counts=bl.counts.astype(np.int32), dq=dq.astype(np.float32), dk=dk.astype(np.float32),
+                        dv=dv.astype(np.float32), route_block=np.int64(RB))
+
+
+def make_ternary(path):
+    rng = np.random.default_rng(5005)
+    # quantize + pack of rows whose entries stay clear of the +-gamma/2 thresholds
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    gamma = np.abs(x).mean(-1, keepdims=True)
+    x = np.where(np.abs(np.abs(x) - 0.5 * gamma) < 1e-3 * gamma, 0.0, x).astype(np.float32)
+    t, g = ot.ternary_quantize(x)
+    out = {"x": x, "packed": ot.pack_ternary(t), "scale": np.asarray(g, dtype=np.float32).reshape(-1)}
+    # prefill over packed K / V: fp16 Q, ternary codes, fp32 row scales, routing + sink + local + shift
+    Z, H, N, D = 1, 2, 384, 64
+    q = rng.standard_normal((Z, H, N, D)).astype(np.float16)
+    kt = rng.integers(-1, 2, size=(Z, H, N, D)).astype(np.float32)
+    vt = rng.integers(-1, 2, size=(Z, H, N, D)).astype(np.float32)
+    ks = (rng.random((Z, H, N)) * 0.6 + 0.1).astype(np.float32)
+    vs = (rng.random((Z, H, N)) * 1.5 + 0.2).astype(np.float32)
+    router = rng.integers(0, 2, size=(Z, H, N // 128, 3), dtype=np.int32)
+    kp, vp = ot.pack_ternary(kt), ot.pack_ternary(vt)
+    ref = ot.ternary_attention_ref(q.astype(np.float32), kp, vp, ks, vs, router, local_window=128, req_depth=2,
+                                   shift_size=77)
+    out.update({"q": q, "k_packed": kp, "v_packed": vp, "k_scale": ks, "v_scale": vs, "router": router,
+                "out": ref.astype(np.float32)})
+    np.savez_compressed(path, **out)
+
+
 if __name__ == "__main__":
     make_block_lists(os.path.join(HERE, "block_lists.npz"))
     make_prefill(os.path.join(HERE, "prefill.npz"))
     make_decode(os.path.join(HERE, "decode.npz"))
+    make_backward(os.path.join(HERE, "backward.npz"))
+    make_ternary(os.path.join(HERE, "ternary.npz"))
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)), "bytes")

@@ -1,6 +1,7 @@
 """The CPU oracle against the committed golden fixtures (tests/golden/*.npz,
-written by tests/golden/make_golden.py): block lists bit-exact, attention and
-decode to float32 storage precision. A change to the oracle that moves any of
+written by tests/golden/make_golden.py): block lists and ternary packing
+bit-exact; attention, decode, backward gradients and the ternary prefill to
+float32 storage precision. A change to the oracle that moves any of
 these fails here."""
 
 import os
@@ -11,6 +12,7 @@ import pytest
 from oracle import attention as oa
 from oracle import blocks as ob
 from oracle import decode as od
+from oracle import ternary as ot
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -66,3 +68,22 @@ def test_decode_fixture(name, kw):
     o = od.decode_reference(q, k, v, g["block_tables"], g["context_lens"], g["router"], g["q_router"], **kw)
     assert np.abs(o - g[f"{name}__out"]).max() <= 1e-6
     assert np.all(o[0] == 0)   # context length 0 -> zeros
+
+
+def test_backward_fixture():
+    g = load("backward.npz")
+    q, k, v, do = (bits_to_f32(g[f"{t}_bits"]) for t in ("q", "k", "v", "do"))
+    mask = ob.lists_to_mask(g["lists"], g["counts"])
+    dq, dk, dv, _ = oa.block_sparse_attention_grad_ref(q, k, v, mask, int(g["route_block"]), do, is_causal=True)
+    for got, name in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert np.abs(got - g[name]).max() <= 1e-5 * max(1.0, np.abs(g[name]).max()), name
+
+
+def test_ternary_fixture():
+    g = load("ternary.npz")
+    t, gamma = ot.ternary_quantize(g["x"])
+    assert np.array_equal(ot.pack_ternary(t), g["packed"])
+    assert np.allclose(np.asarray(gamma).reshape(-1), g["scale"], rtol=1e-6)
+    ref = ot.ternary_attention_ref(g["q"].astype(np.float32), g["k_packed"], g["v_packed"], g["k_scale"],
+                                   g["v_scale"], g["router"], local_window=128, req_depth=2, shift_size=77)
+    assert np.abs(ref - g["out"]).max() <= 1e-6
