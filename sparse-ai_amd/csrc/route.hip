@@ -16,6 +16,8 @@
 // kernel is HBM-bound: B H S L p element reads for the whole batch.
 #include "sa_internal.h"
 
+#include <type_traits>
+
 namespace sa {
 namespace {
 
@@ -30,6 +32,23 @@ struct VoteParams {
   int32_t* out;
 };
 
+// Four consecutive scores, 4 * sizeof(T)-aligned, as floats.
+template <typename T>
+__device__ __forceinline__ void load4(const T* src, float (&x)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 v = *reinterpret_cast<const float4*>(src);
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2*>(src);
+    const uint32_t h[4] = {u.x & 0xffffu, u.x >> 16, u.y & 0xffffu, u.y >> 16};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if constexpr (std::is_same<T, bf16_t>::value) x[c] = bf16_bits_to_float(h[c]);
+      else x[c] = f16_bits_to_float(h[c]);
+    }
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kVoteThreads) void route_vote_kernel(VoteParams p) {
   __shared__ int votes[kMaxR][kMaxP];
@@ -42,16 +61,30 @@ __global__ __launch_bounds__(kVoteThreads) void route_vote_kernel(VoteParams p) 
   const int t0 = i * p.RB;
   const int len = min(p.RB, p.S - t0);
   const T* base = static_cast<const T*>(p.a) + b * p.s0 + h * p.s1;
+  // Four contiguous, aligned branch scores: one vector read per (token, level).
+  constexpr int kVec4 = 4 * static_cast<int>(sizeof(T));
+  const bool vec4 = p.P == 4 && p.s4 == 1 && (p.s0 * sizeof(T)) % kVec4 == 0 && (p.s1 * sizeof(T)) % kVec4 == 0 &&
+                    (p.s2 * sizeof(T)) % kVec4 == 0 && (p.s3 * sizeof(T)) % kVec4 == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.a) % kVec4) == 0;
   for (int j = threadIdx.x; j < len * p.R; j += kVoteThreads) {
     const int t = t0 + j / p.R, l = j % p.R;
     const T* row = base + t * p.s2 + l * p.s3;
-    float best = Elem<T>::load(row);
+    float x[4];
     int arg = 0;
-    for (int c = 1; c < p.P; ++c) {
-      const float x = Elem<T>::load(row + c * p.s4);
-      if (x > best) {   // first maximum wins ties
-        best = x;
-        arg = c;
+    if (vec4) {
+      load4<T>(row, x);
+#pragma unroll
+      for (int c = 1; c < 4; ++c) {
+        if (x[c] > x[arg]) arg = c;   // first maximum wins ties
+      }
+    } else {
+      float best = Elem<T>::load(row);
+      for (int c = 1; c < p.P; ++c) {
+        const float y = Elem<T>::load(row + c * p.s4);
+        if (y > best) {   // first maximum wins ties
+          best = y;
+          arg = c;
+        }
       }
     }
     atomicAdd(&votes[l][arg], 1);
