@@ -10,6 +10,8 @@ sum(counts) (every listed 128x128 tile counted in full).
 
 Also reported: the prefill kernel alone (HIP events around back-to-back
 launches on its stream; `roofline` is built from it), the list build alone,
+the same step in one launch (routed_block_attention with the branch arity:
+the build runs inside the prefill kernel),
 sparse paged decode on config 4 (GB/s of routed KV bytes), the backward on
 config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), the
 ternary packed-K/V prefill over config 2's lists, one config-5 surgery layer
@@ -187,7 +189,7 @@ def main():
     import torch
 
     import sparse_workloads as wl
-    from ultrametric import block_list_attention, build_block_lists, ultrametric_decode
+    from ultrametric import block_list_attention, build_block_lists, routed_block_attention, ultrametric_decode
     from ultrametric import _native as nat
 
     if not torch.cuda.is_available():
@@ -218,8 +220,11 @@ def main():
     useful = wl.useful_prefill_flops(mask, RB, N, D, True)
 
     def step():
-        b = build()
-        return block_list_attention(q, k, v, b, route_block=RB, is_causal=True)
+        return block_list_attention(q, k, v, build(), route_block=RB, is_causal=True)
+
+    def step_fused():
+        # the same step in one launch: the list build runs inside the prefill kernel
+        return routed_block_attention(q, k, v, router, 2, route_block=RB, is_causal=True, sink_block=True, arity=4)
 
     with torch.no_grad():
         spin_steps = spin_up(step, args.spinup_ms, torch)   # untimed, before the warmup steps
@@ -238,26 +243,52 @@ def main():
         ms_step = s.elapsed_time(e) / args.steps
         log(f"timed {args.steps} steps: {ms_step * 1e3:.1f} us/step (wall {wall * 1e3 / args.steps * 1e3:.1f} us)")
 
-        # prefill kernel alone (lists prebuilt), raw ABI launches back to back
+        reps = max(50, args.steps)
+        fused_step_ms = time_launches(step_fused, reps, torch)
+        assert torch.equal(step(), step_fused()), "fused step disagrees with the two-launch step"
+
+        # raw ABI launches of the fused build + prefill, back to back
         out = torch.empty_like(q)
-        lists = bl.lists.contiguous()
+        lists_f = torch.empty_like(bl.lists)
+        counts_f = torch.empty_like(counts)
         st = [nat.strides(t) for t in (q, k, v, out)]
         lib = nat.lib()
         scale = 1.0 / math.sqrt(D)
         stream = nat.stream(dev)
 
-        def fwd():
-            nat.check(lib.sa_block_sparse_fwd(nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), None,
-                                              nat.ptr(lists), nat.ptr(counts), None, 0, Z, H, H, N, D, RB,
-                                              bl.max_count, st[0], st[1], st[2], st[3], None, scale, 1, 1,
-                                              stream))
+        # arguments converted once: the launches, not Python call overhead
+        fargs = (nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), None, nat.ptr(router),
+                 nat.DTYPE_CODES[router.dtype], nat.strides(router), router.shape[-1], None, 2, 4, 1, 0,
+                 nat.ptr(lists_f), nat.ptr(counts_f), Z, H, H, N, D, RB, st[0], st[1], st[2], st[3], scale, 1, 1,
+                 stream)
+        fused_fn = lib.sa_routed_block_sparse_fwd
 
-        reps = max(50, args.steps)
-        fwd_ms = time_launches(fwd, reps, torch)
+        def fused():
+            nat.check(fused_fn(*fargs))
+
+        # the step's dominant kernel: the prefill over prebuilt lists, raw ABI launches
+        lists = bl.lists.contiguous()
+        out2 = torch.empty_like(q)
+
+        pargs = (nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out2), None, nat.ptr(lists), nat.ptr(counts), None,
+                 0, Z, H, H, N, D, RB, bl.max_count, st[0], st[1], st[2], st[3], None, scale, 1, 1, stream)
+        fwd_fn = lib.sa_block_sparse_fwd
+
+        def fwd():
+            nat.check(fwd_fn(*pargs))
+
+        # alternating rounds, medians: a single block can catch a transient clock state
+        fl, pl = [], []
+        for _ in range(3):
+            fl.append(time_launches(fused, reps, torch))
+            pl.append(time_launches(fwd, reps, torch))
+        fused_ms, fwd_ms = sorted(fl)[1], sorted(pl)[1]
         build_ms = time_launches(build, reps, torch)
         ref_out = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True)
-        assert torch.equal(out, ref_out), "raw-ABI launch disagrees with the public API"
-    log(f"prefill kernel {fwd_ms * 1e3:.1f} us, build {build_ms * 1e3:.1f} us")
+        assert torch.equal(out, ref_out) and torch.equal(out2, ref_out), "raw-ABI launch disagrees with the API"
+        assert torch.equal(lists_f, bl.lists) and torch.equal(counts_f, counts), "fused lists differ"
+    log(f"prefill kernel {fwd_ms * 1e3:.1f} us, build {build_ms * 1e3:.1f} us; fused build + prefill: kernel "
+        f"{fused_ms * 1e3:.1f} us, step {fused_step_ms * 1e3:.1f} us")
 
     value = flop_alg / (ms_step * 1e-3) / 1e12
     achieved = flop_alg / (fwd_ms * 1e-3) / 1e12
@@ -286,6 +317,8 @@ def main():
         },
         "prefill_kernel_ms": round(fwd_ms, 5),
         "build_ms": round(build_ms, 5),
+        "fused_build_prefill": {"kernel_ms": round(fused_ms, 5), "ms_per_step": round(fused_step_ms, 5),
+                                "api": "routed_block_attention(..., arity=4): one launch, lists written out"},
         "roofline": {
             "kernel": "prefill_mfma_kernel<bf16, D=128, 4 waves, causal>",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",

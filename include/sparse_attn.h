@@ -130,6 +130,32 @@ int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, 
                         int dtype, int is_causal, void* stream);
 
 /*
+ * Routed block-sparse prefill with the list build fused into the forward.
+ * Replaces: routed_block_attention (src/ultrametric/block_list.py:1064-1083)
+ * when the caller knows the branch arity, i.e. build_block_lists(...,
+ * arity=base) (block_list.py:170-278, sync-free) followed by
+ * block_list_attention (block_list.py:968-1061), in one launch.
+ * Each workgroup builds its row's list from the routing ids (code matching,
+ * then local band, sink column and causal mask, as sa_build_block_lists) and
+ * writes it to lists (Z, H, NB, NB) int32 contiguous, zero padded, and
+ * counts (Z, H, NB): the sync-free BlockLists, usable by the backward.
+ * router, router_dtype, router_strides, TD, depth_dev, depth_uniform, base:
+ * as sa_build_block_lists with use_codes = 1 (TD * log2(base) < 62 is the
+ * caller's condition for that, as in the reference).
+ * Supported: bf16 / f16, D in {32, 64, 128}, route block >= 32, no soft
+ * bias, NB <= 256 (route block >= 128), 128 (64) or 64 (32). Otherwise
+ * SA_EUNSUPPORTED: build the lists and call sa_block_sparse_fwd instead.
+ */
+int sa_routed_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                               const void* router, int router_dtype, const int64_t* router_strides, int TD,
+                               const int64_t* depth_dev, int depth_uniform, int64_t base, int sink_block,
+                               int local_blocks, int32_t* lists, int32_t* counts, int Z, int H, int H_kv,
+                               int N, int D, int route_block, const int64_t* q_strides,
+                               const int64_t* k_strides, const int64_t* v_strides,
+                               const int64_t* o_strides, float sm_scale, int dtype, int is_causal,
+                               void* stream);
+
+/*
  * Transposed block lists: per (z, h, key block), the ascending query blocks
  * whose lists hold it.
  * Replaces: build_transposed_block_lists (src/ultrametric/block_list.py:281-327),

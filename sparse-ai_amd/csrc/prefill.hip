@@ -55,6 +55,15 @@ struct FwdParams {
   int is_causal;
   int mtiles;      // query tiles per (z, h)
   int total_wg;
+  // Fused list build (sa_routed_block_sparse_fwd): routing ids -> each row's
+  // list in the kernel, written back to lists_out / counts_out.
+  const void* router;
+  int64_t rs0, rs1, rs2, rs3;
+  int router_i64, TD, depth_uniform, sink, local;
+  const int64_t* depth_dev;
+  uint64_t base;
+  int32_t* lists_out;
+  int32_t* counts_out;
 };
 
 __device__ __forceinline__ float load_bias(const FwdParams& p, int z, int h, int qb, int t) {
@@ -177,7 +186,9 @@ __global__ __launch_bounds__(256) void prefill_generic_kernel(FwdParams p) {
 
 // S: pipeline stages (K+V tiles of BN keys; S - 1 in flight while one is
 // computed). WPE: waves per SIMD the register budget is sized for.
-template <typename T, int D, int NW, bool CAUSAL, int S, int WPE>
+// FUSED: the row's block list is built in the kernel from the routing ids
+// (sync-free, code matching, NB <= 64 NW) instead of read from p.lists.
+template <typename T, int D, int NW, bool CAUSAL, int S, int WPE, bool FUSED>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE)))
 void prefill_mfma_kernel(FwdParams p) {
   constexpr int BN = 32;               // keys per pipeline stage
@@ -201,6 +212,7 @@ void prefill_mfma_kernel(FwdParams p) {
   __shared__ __attribute__((aligned(1024))) char stage_lds[S * STAGEB];
   __shared__ int32_t list_lds[kListSeg];
   __shared__ float bias_lds[kListSeg];
+  __shared__ int32_t wave_hits[NW];
 
   const int work = xcd_remap(blockIdx.x, p.total_wg);
   const int zh = work / p.mtiles;
@@ -209,7 +221,7 @@ void prefill_mfma_kernel(FwdParams p) {
   const int m0 = mt * BM;
   const int qb = m0 / p.RB;
   const int64_t row = static_cast<int64_t>(zh) * p.NB + qb;
-  const int count = min(max(p.counts[row], 0), p.max_count);
+  int count = FUSED ? 0 : min(max(p.counts[row], 0), p.max_count);
   const int32_t* list = p.lists + row * p.max_count;
   const int spb = p.RB / BN;
   const int lspb = __builtin_ctz(spb);   // spb = route_block / 32 is a power of two
@@ -340,8 +352,65 @@ void prefill_mfma_kernel(FwdParams p) {
   // arrived. The row has max_count readable entries; issue() clamps any key
   // out of range, so this is safe for short or empty rows too (loads that no
   // tile consumes are drained before the kernel ends).
-  const int e0 = p.max_count > 0 ? list[0] : 0;
-  const int e1 = p.max_count > 1 ? list[1] : 0;
+  if constexpr (FUSED) {
+    // This row's list from the routing ids, as build_block_lists does with
+    // `arity` (block_list.py:212-229,263-278): code = sum_l id_l [l < depth]
+    // base^l (wrapping 64-bit), match = equal codes, then local band OR, sink
+    // OR, causal AND; key block kb is thread kb (NB <= NT), the ballot and the
+    // waves' hit counts give its slot. The first query tile of the route
+    // block writes the row back (sync-free layout: NB columns, zero padded).
+    const int depth = p.depth_dev ? static_cast<int>(p.depth_dev[h]) : p.depth_uniform;
+    auto code_of = [&](int blk) {
+      uint64_t code = 0, pw = 1;
+      for (int l = 0; l < p.TD; ++l) {
+        if (l < depth) {
+          const int64_t off = z * p.rs0 + h * p.rs1 + blk * p.rs2 + l * p.rs3;
+          const int64_t id = p.router_i64 ? static_cast<const int64_t*>(p.router)[off]
+                                          : static_cast<int64_t>(static_cast<const int32_t*>(p.router)[off]);
+          code += static_cast<uint64_t>(id) * pw;
+        }
+        pw *= p.base;
+      }
+      return code;
+    };
+    const int kb = tid;
+    bool m = false;
+    if (kb < p.NB) {
+      m = code_of(kb) == code_of(qb);
+      const int diff = qb > kb ? qb - kb : kb - qb;
+      if (p.local > 0 && diff <= p.local) m = true;
+      if (p.sink && kb == 0) m = true;
+      if (CAUSAL && kb > qb) m = false;
+    }
+    const uint64_t hits = __ballot(m);
+    if (lane == 0) wave_hits[wave] = static_cast<int>(__popcll(hits));
+    __syncthreads();
+    int before = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int c = wave_hits[w];
+      before += w < wave ? c : 0;
+      count += c;
+    }
+    const int pos = before + static_cast<int>(__builtin_amdgcn_mbcnt_hi(
+                                 static_cast<uint32_t>(hits >> 32),
+                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(hits), 0u)));
+    if (m) {
+      list_lds[pos] = kb;
+      bias_lds[pos] = 0.f;
+    }
+    if (m0 % p.RB == 0 && kb < p.NB) {
+      int32_t* out_row = p.lists_out + row * p.NB;
+      if (m) out_row[pos] = kb;
+      if (kb >= count) out_row[kb] = 0;
+      if (kb == 0) p.counts_out[row] = count;
+    }
+    __syncthreads();
+  }
+  const int e0 = FUSED ? (count > 0 ? __builtin_amdgcn_readfirstlane(list_lds[0]) : 0)
+                       : (p.max_count > 0 ? list[0] : 0);
+  const int e1 = FUSED ? (count > 1 ? __builtin_amdgcn_readfirstlane(list_lds[1]) : e0)
+                       : (p.max_count > 1 ? list[1] : 0);
   auto early_key = [&](int m) { return ((m >> lspb) == 0 ? e0 : e1) * p.RB + (m & (spb - 1)) * BN; };
 #pragma unroll
   for (int st0 = 0; st0 < S - 1; ++st0) issue(early_key(st0), st0);
@@ -424,9 +493,11 @@ void prefill_mfma_kernel(FwdParams p) {
   for (int seg = 0; seg < count; seg += kListSeg) {
     const int seg_n = min(count - seg, kListSeg);
     if (seg > 0) __syncthreads();   // every wave is done with the previous segment
-    for (int t = tid; t < seg_n; t += NT) {
-      list_lds[t] = list[seg + t];
-      bias_lds[t] = p.sb ? load_bias(p, z, h, qb, seg + t) : 0.f;
+    if constexpr (!FUSED) {
+      for (int t = tid; t < seg_n; t += NT) {
+        list_lds[t] = list[seg + t];
+        bias_lds[t] = p.sb ? load_bias(p, z, h, qb, seg + t) : 0.f;
+      }
     }
     __syncthreads();
     // No compiler-visible load may be outstanding once the pipeline runs (the
@@ -519,10 +590,17 @@ void launch_mfma_shape(FwdParams& p, hipStream_t stream) {
   p.mtiles = (p.N + NW * 32 - 1) / (NW * 32);
   p.total_wg = p.Z * p.H * p.mtiles;
   dim3 g(p.total_wg), b(NW * 64);
+  if (p.router) {
+    if (p.is_causal)
+      hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, true, S, WPE, true>), g, b, 0, stream, p);
+    else
+      hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, false, S, WPE, true>), g, b, 0, stream, p);
+    return;
+  }
   if (p.is_causal)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, true, S, WPE>), g, b, 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, true, S, WPE, false>), g, b, 0, stream, p);
   else
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, false, S, WPE>), g, b, 0, stream, p);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, NW, false, S, WPE, false>), g, b, 0, stream, p);
 }
 
 // Three pipeline stages (48 KB of LDS at D = 128) and a register budget of
@@ -556,15 +634,27 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 }  // namespace
 }  // namespace sa
 
-extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out,
-                                   float* lse, const int32_t* lists, const int32_t* counts,
-                                   const void* soft_bias, int soft_bias_dtype, int Z, int H,
-                                   int H_kv, int N, int D, int route_block, int max_count,
-                                   const int64_t* q_strides, const int64_t* k_strides,
-                                   const int64_t* v_strides, const int64_t* o_strides,
-                                   const int64_t* sb_strides, float sm_scale, int dtype,
-                                   int is_causal, void* stream) {
-  using namespace sa;
+namespace sa {
+namespace {
+
+// Routing ids of the fused entry point (sa_routed_block_sparse_fwd).
+struct FusedRouting {
+  const void* router;
+  int router_dtype;
+  const int64_t* strides;
+  int TD;
+  const int64_t* depth_dev;
+  int depth_uniform;
+  int64_t base;
+  int sink_block, local_blocks;
+};
+
+int fwd_impl(const void* q, const void* k, const void* v, void* out, float* lse, const int32_t* lists,
+             const int32_t* counts, const void* soft_bias, int soft_bias_dtype, int Z, int H, int H_kv, int N,
+             int D, int route_block, int max_count, const int64_t* q_strides, const int64_t* k_strides,
+             const int64_t* v_strides, const int64_t* o_strides, const int64_t* sb_strides, float sm_scale,
+             int dtype, int is_causal, void* stream, const FusedRouting* fz, int32_t* lists_out,
+             int32_t* counts_out) {
   if (!q_strides || !k_strides || !v_strides || !o_strides) return fail(SA_EINVAL, "NULL strides");
   if (Z < 0 || H < 0 || N < 0 || H_kv <= 0 || (H > 0 && H % H_kv != 0)) {
     return fail(SA_EINVAL, "bad Z/H/H_kv/N");
@@ -622,10 +712,74 @@ extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, 
   const long long wg = static_cast<long long>(Z) * H * ((N + 15) / 16);
   if (wg > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
 
+  if (fz) {
+    // The fused build runs inside the MFMA kernel: one key block per thread.
+    const int nt = 64 * (route_block % 128 == 0 ? 4 : (route_block == 64 ? 2 : 1));
+    if (!mfma_ok || soft_bias || p.NB > nt) {
+      return fail(SA_EUNSUPPORTED, "fused list build needs the MFMA path, no soft bias and NB <= " +
+                                       std::to_string(nt));
+    }
+    p.router = fz->router;
+    p.rs0 = fz->strides[0]; p.rs1 = fz->strides[1]; p.rs2 = fz->strides[2]; p.rs3 = fz->strides[3];
+    p.router_i64 = fz->router_dtype == SA_DTYPE_I64;
+    p.TD = fz->TD;
+    p.depth_dev = fz->depth_dev;
+    p.depth_uniform = fz->depth_uniform;
+    p.base = static_cast<uint64_t>(fz->base);
+    p.sink = fz->sink_block != 0;
+    p.local = fz->local_blocks;
+    p.lists_out = lists_out;
+    p.counts_out = counts_out;
+  }
   if (mfma_ok) {
     return dtype == SA_DTYPE_BF16 ? launch_mfma<bf16_t>(p, D, s) : launch_mfma<f16_t>(p, D, s);
   }
   if (dtype == SA_DTYPE_F32) return launch_generic<float>(p, D, s);
   if (dtype == SA_DTYPE_BF16) return launch_generic<bf16_t>(p, D, s);
   return launch_generic<f16_t>(p, D, s);
+}
+
+}  // namespace
+}  // namespace sa
+
+extern "C" int sa_block_sparse_fwd(const void* q, const void* k, const void* v, void* out,
+                                   float* lse, const int32_t* lists, const int32_t* counts,
+                                   const void* soft_bias, int soft_bias_dtype, int Z, int H,
+                                   int H_kv, int N, int D, int route_block, int max_count,
+                                   const int64_t* q_strides, const int64_t* k_strides,
+                                   const int64_t* v_strides, const int64_t* o_strides,
+                                   const int64_t* sb_strides, float sm_scale, int dtype,
+                                   int is_causal, void* stream) {
+  return sa::fwd_impl(q, k, v, out, lse, lists, counts, soft_bias, soft_bias_dtype, Z, H, H_kv, N, D,
+                      route_block, max_count, q_strides, k_strides, v_strides, o_strides, sb_strides, sm_scale,
+                      dtype, is_causal, stream, nullptr, nullptr, nullptr);
+}
+
+extern "C" int sa_routed_block_sparse_fwd(const void* q, const void* k, const void* v, void* out, float* lse,
+                                          const void* router, int router_dtype, const int64_t* router_strides,
+                                          int TD, const int64_t* depth_dev, int depth_uniform, int64_t base,
+                                          int sink_block, int local_blocks, int32_t* lists, int32_t* counts,
+                                          int Z, int H, int H_kv, int N, int D, int route_block,
+                                          const int64_t* q_strides, const int64_t* k_strides,
+                                          const int64_t* v_strides, const int64_t* o_strides, float sm_scale,
+                                          int dtype, int is_causal, void* stream) {
+  using namespace sa;
+  if (router_dtype != SA_DTYPE_I32 && router_dtype != SA_DTYPE_I64) {
+    return fail(SA_EINVAL, "router ids must be int32 or int64");
+  }
+  if (TD < 1) return fail(SA_EINVAL, "tree depth must be >= 1");
+  if (!depth_dev && (depth_uniform < 0 || depth_uniform > TD)) {
+    return fail(SA_EINVAL, "req_depth out of range [0, TD]");
+  }
+  if (base < 2) return fail(SA_EINVAL, "code base must be >= 2");
+  if (local_blocks < 0) return fail(SA_EINVAL, "local_blocks must be >= 0");
+  const long long NB = route_block > 0 ? (static_cast<long long>(N) + route_block - 1) / route_block : 0;
+  if (static_cast<long long>(Z) * H * N > 0 && (!router || !router_strides || !lists || !counts)) {
+    return fail(SA_EINVAL, "NULL router / lists / counts");
+  }
+  const FusedRouting fz{router, router_dtype, router_strides, TD, depth_dev, depth_uniform, base, sink_block,
+                        local_blocks};
+  return fwd_impl(q, k, v, out, lse, lists, counts, nullptr, 0, Z, H, H_kv, N, D, route_block,
+                  static_cast<int>(NB), q_strides, k_strides, v_strides, o_strides, nullptr, sm_scale, dtype,
+                  is_causal, stream, &fz, lists, counts);
 }

@@ -36,6 +36,9 @@ _SIGNATURES = {
     "sa_build_block_lists_mask": (_I, [_P, _I64P, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P]),
     "sa_block_sparse_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                  _I64P, _I64P, _I64P, _I64P, _I64P, ctypes.c_float, _I, _I, _P]),
+    "sa_routed_block_sparse_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I64P, _I, _P, _I, _I64, _I, _I, _P, _P,
+                                        _I, _I, _I, _I, _I, _I, _I64P, _I64P, _I64P, _I64P, ctypes.c_float, _I,
+                                        _I, _P]),
     "sa_decode_workspace_bytes": (ctypes.c_size_t, [_I, _I, _I, _I, _I]),
     "sa_sparse_paged_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                     _I, _I, _I, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,

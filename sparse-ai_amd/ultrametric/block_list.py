@@ -557,13 +557,69 @@ def routed_block_attention(
     local_blocks: int = 0,
     sm_scale: Optional[float] = None,
     soft_block_bias: Optional[torch.Tensor] = None,
+    arity: Optional[int] = None,
 ) -> torch.Tensor:
-    """Build the block lists, then run the kernel (block_list.py:1064-1083)."""
+    """Build the block lists, then run the kernel (block_list.py:1064-1083).
+
+    ``arity`` (extension; the branch count, ids in [0, arity)) builds the lists
+    sync-free, as ``build_block_lists(..., arity=arity)``. Then, without a soft
+    bias and when no input needs a gradient, the build runs inside the forward
+    kernel: one launch (``sa_routed_block_sparse_fwd``) instead of two.
+    """
+    if arity is not None and soft_block_bias is None and not (
+            torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)):
+        fused = _routed_fused(q, k, v, router_indices, req_depth, route_block=route_block, is_causal=is_causal,
+                              sink_block=sink_block, local_blocks=local_blocks, sm_scale=sm_scale, arity=arity)
+        if fused is not None:
+            return fused[0]
     bl = build_block_lists(router_indices, req_depth, is_causal=is_causal,
-                           sink_block=sink_block, local_blocks=local_blocks)
+                           sink_block=sink_block, local_blocks=local_blocks, arity=arity)
     return block_list_attention(q, k, v, bl, route_block=route_block,
                                 is_causal=is_causal, sm_scale=sm_scale,
                                 soft_block_bias=soft_block_bias)
+
+
+def _routed_fused(q, k, v, router_indices, req_depth, *, route_block, is_causal, sink_block, local_blocks,
+                  sm_scale, arity):
+    """(out, BlockLists) from one sa_routed_block_sparse_fwd launch, or None when the
+    inputs are outside what it covers (the caller then builds the lists and calls
+    block_list_attention, which also raises the reference's errors)."""
+    if not HAS_TRITON or router_indices.dim() != 4 or q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
+        return None
+    Z, H, N, D = q.shape
+    if (q.dtype not in (torch.bfloat16, torch.float16) or not (q.dtype == k.dtype == v.dtype)
+            or k.shape[0] != Z or k.shape[2:] != q.shape[2:] or k.shape[1] == 0 or H % k.shape[1] != 0
+            or route_block < 32 or route_block & (route_block - 1) or D & (D - 1) or D < 16):
+        return None
+    Zr, Hr, NB, TD = router_indices.shape
+    if (Zr, Hr, NB) != (Z, H, -(-N // route_block)) or TD < 1:
+        return None
+    base = max(2, int(arity))
+    if not TD * math.log2(base) < 62:
+        return None
+    if isinstance(req_depth, int):
+        if not 0 <= req_depth <= TD:
+            return None
+        depth_dev, depth_uniform = None, int(req_depth)
+    else:
+        depth_dev, depth_uniform = _depth_tensor(req_depth, H, TD, q.device), 0
+    r = router_indices if router_indices.dtype in (torch.int32, torch.int64) else router_indices.to(torch.int64)
+    dev = nat.require_device(q, k, v, r)
+    out = torch.empty((Z, H, N, D), dtype=q.dtype, device=dev)
+    lists = torch.empty((Z, H, NB, NB), dtype=torch.int32, device=dev)
+    counts = torch.empty((Z, H, NB), dtype=torch.int32, device=dev)
+    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(D)
+    with torch.cuda.device(dev):
+        rc = nat.lib().sa_routed_block_sparse_fwd(
+            nat.ptr(q), nat.ptr(k), nat.ptr(v), nat.ptr(out), None, nat.ptr(r), nat.DTYPE_CODES[r.dtype],
+            nat.strides(r), TD, nat.ptr(depth_dev), depth_uniform, base, int(bool(sink_block)), int(local_blocks),
+            nat.ptr(lists), nat.ptr(counts), Z, H, k.shape[1], N, D, int(route_block), nat.strides(q),
+            nat.strides(k), nat.strides(v), nat.strides(out), float(scale), nat.DTYPE_CODES[q.dtype],
+            int(bool(is_causal)), nat.stream(dev))
+    if rc == nat.SA_EUNSUPPORTED:
+        return None
+    nat.check(rc)
+    return out, BlockLists(lists, counts, NB)
 
 
 # ----------------------------------------------------------------------------
