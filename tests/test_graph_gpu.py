@@ -1,5 +1,6 @@
 """The per-layer surgery step (route vote, sync-free list build, prefill
-forward) and a serving decode step captured in a HIP graph: every replay, with
+forward), the fused one-launch routed prefill and a serving decode step
+captured in a HIP graph: every replay, with
 new inputs copied into the captured buffers and eager work plus
 synchronisations between replays, equals the eager result bit for bit (the
 kernels are deterministic and launch nothing outside the captured stream)."""
@@ -74,3 +75,37 @@ def test_decode_step_in_graph():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_fused_routed_prefill_in_graph():
+    # routed_block_attention with the arity: list build and prefill in one launch, no host read
+    from ultrametric import routed_block_attention
+    g = torch.Generator().manual_seed(4)
+    Z, H, N, D, rb = 1, 4, 2048, 128, 128
+    q = torch.empty(Z, H, N, D, dtype=torch.bfloat16, device=DEV)
+    k = torch.empty_like(q)
+    v = torch.empty_like(q)
+    router = torch.empty(Z, H, N // rb, 3, dtype=torch.int32, device=DEV)
+
+    def fill():
+        for t in (q, k, v):
+            t.copy_(torch.randn(t.shape, generator=g).to(t.dtype))
+        router.copy_(torch.randint(0, 4, router.shape, generator=g, dtype=torch.int32))
+
+    def step():
+        return routed_block_attention(q, k, v, router, 2, route_block=rb, is_causal=True, sink_block=True, arity=4)
+
+    with torch.no_grad():
+        fill()
+        step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = step()
+        for _ in range(3):
+            fill()
+            eager = step()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
