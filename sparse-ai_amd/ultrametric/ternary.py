@@ -19,8 +19,8 @@ import torch
 from . import _native as nat
 from .block_list import build_block_lists
 
-__all__ = ["ternary_quantize_pack", "pack_ternary", "unpack_ternary", "ternary_ultrametric_attention",
-           "ternary_ultrametric_attention_triton"]
+__all__ = ["ternary_quantize_pack", "pack_ternary", "unpack_ternary", "ternary_block_lists",
+           "ternary_ultrametric_attention", "ternary_ultrametric_attention_triton"]
 
 
 def _pack(x: torch.Tensor, mode: int):
@@ -61,6 +61,22 @@ def unpack_ternary(packed: torch.Tensor, original_shape: tuple) -> torch.Tensor:
     return torch.where(vals == 2, torch.full_like(vals, -1.0), torch.where(vals == 1, vals, torch.zeros_like(vals)))
 
 
+# The reference kernel compares routing ids level by level (kernel.py:197-201),
+# whatever `p` is. A sync-free build with this base never takes the mixed-radix
+# code path for TD >= 2 (TD * 31 >= 62) and, for TD = 1, codes each id as
+# itself: level-wise equality, with no aliasing of ids >= p and no host read.
+_LEVELWISE_ARITY = 1 << 31
+
+
+def ternary_block_lists(router: torch.Tensor, req_depth: int, local_window: int = 128):
+    """The visited (query block, key block) pairs of the ternary prefill as
+    sync-free BlockLists (route block 128): the first req_depth routing levels
+    equal, or the sink block, or within ceil(local_window / 128) blocks, causal
+    (kernel.py:193-208)."""
+    return build_block_lists(router, req_depth, is_causal=True, sink_block=True,
+                             local_blocks=math.ceil(local_window / 128), arity=_LEVELWISE_ARITY)
+
+
 def ternary_ultrametric_attention(
     q: torch.Tensor,
     k_packed: torch.Tensor,
@@ -77,8 +93,10 @@ def ternary_ultrametric_attention(
 
     q: (Z, H, N, D) fp16; k_packed / v_packed: (Z, H_kv, N, D / 16) int32;
     k_scale / v_scale: (Z, H_kv, N); router_indices: (Z, H, NB', TD) branch ids
-    in [0, p) (rows past NB' count as zeros, as the reference pads them).
-    Returns (Z, H, N, D) fp16.
+    (rows past NB' count as zeros, as the reference pads them). Blocks match
+    when their first req_depth ids are equal, level by level, as in the
+    reference; ``p`` is accepted for its signature and does not enter the
+    match. Returns (Z, H, N, D) fp16.
     """
     if q.dtype != torch.float16:
         raise ValueError(f"ternary attention requires float16 Q, got {q.dtype}")
@@ -98,8 +116,7 @@ def ternary_ultrametric_attention(
         r = torch.cat([r, torch.zeros((Z, H, NB - r.shape[2], TD), dtype=torch.int32, device=dev)], dim=2)
     r = r[:, :, :NB]
     depth = min(max(int(req_depth), 0), TD)
-    bl = build_block_lists(r, depth, is_causal=True, sink_block=True,
-                           local_blocks=math.ceil(local_window / 128), arity=max(2, int(p)))
+    bl = ternary_block_lists(r, depth, local_window)
     ks = k_scale if k_scale.dtype in (torch.float32, torch.bfloat16, torch.float16) else k_scale.float()
     vs = v_scale if v_scale.dtype == ks.dtype else v_scale.to(ks.dtype)
     qc = q if q.stride(-1) == 1 else q.contiguous()

@@ -98,3 +98,17 @@ def test_quantized_kv_round_trip_through_attention():
     ref = ot.ternary_attention_ref(q.float().cpu().numpy(), kp.cpu().numpy(), vp.cpu().numpy(), ks.cpu().numpy(),
                                    vs.cpu().numpy(), router.numpy())
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 5e-3 * max(1.0, np.abs(ref).max())
+
+
+def test_ids_above_the_arity_match_level_by_level():
+    # the reference compares routing ids level by level whatever p is: ids >= p
+    # (here 0..3 with the default p = 2) must not alias into extra matches
+    q, kp, vp, ks, vs, router = make(1, 2, 2, 1024, 64, seed=21, TD=3, p=4)
+    out = ternary_ultrametric_attention(q.to(DEV), torch.from_numpy(kp).to(DEV), torch.from_numpy(vp).to(DEV),
+                                        ks.to(DEV), vs.to(DEV), router.to(DEV), req_depth=2)
+    ref = oracle(q, kp, vp, ks, vs, router, 1, req_depth=2)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= 5e-3 * max(1.0, np.abs(ref).max())
+    from ultrametric.ternary import ternary_block_lists
+    bl = ternary_block_lists(router.to(DEV), 2, 128)
+    sel = ot.block_selection(router.numpy(), 2, 128, router.shape[2])
+    assert int(bl.counts.sum()) == int(sel.sum())
