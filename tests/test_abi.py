@@ -155,3 +155,23 @@ def test_empty_problems_accept_null_data():
     dec = [N0] * 8 + [0, 8, 2, 64, 16, 3, 2, 4, 2, 0, 0] + s[:7] + [N0, 0, 1, None]
     assert lib.sa_sparse_paged_decode(*dec) == nat.SA_OK
     assert lib.sa_block_sparse_bwd_plan_bytes(0, 2, 2, 64, 64, 1) == 0
+
+
+def test_routed_fwd_argument_errors():
+    lib = nat.lib()
+    p = ctypes.c_void_p(256)
+
+    def call(router_dtype=3, TD=3, depth=2, base=4, local=0, Z=1, H=2, N=1024, D=128, rb=128, dtype=1):
+        rs = (ctypes.c_int64 * 4)(H * 400 * TD, 400 * TD, TD, 1)
+        qs = (ctypes.c_int64 * 4)(H * N * D, N * D, D, 1)      # contiguous (Z, H, N, D)
+        return lib.sa_routed_block_sparse_fwd(p, p, p, p, None, p, router_dtype, rs, TD, None, depth, base, 1,
+                                              local, p, p, Z, H, H, N, D, rb, qs, qs, qs, qs, 0.1, dtype, 1, None)
+    assert call(router_dtype=0) == nat.SA_EINVAL          # float router ids
+    assert call(TD=0) == nat.SA_EINVAL
+    assert call(depth=4) == nat.SA_EINVAL                 # depth beyond TD
+    assert call(base=1) == nat.SA_EINVAL
+    assert call(local=-1) == nat.SA_EINVAL
+    assert call(dtype=0) == nat.SA_EUNSUPPORTED           # fp32: the MFMA path only
+    assert call(N=40000) == nat.SA_EUNSUPPORTED           # NB = 313 > 256 key blocks per workgroup
+    assert b"NB" in lib.sa_last_error()
+    assert call(Z=0) == nat.SA_OK                         # empty problem: no launch
