@@ -18,8 +18,9 @@
 //     block-table entry, then lane j loads head j's routing vector (one
 //     16-byte load when the router rows allow it, so a page's G vectors are
 //     one contiguous read); a ballot turns the G match bits into the page's
-//     head mask (forced pages: all heads). All 16 passes of a range issue
-//     their loads back to back;
+//     head mask (forced pages: all heads). The passes of a range run in
+//     groups of 16 (two groups, 2048 pages, at G = 4); a group issues its
+//     loads back to back;
 //   phase A2 — the selected pages are compacted into LDS in ascending logical
 //     order (per-thread counts, wave prefix sum, per-wave offsets);
 //   phase B — the 4 waves take selected pages round-robin with up to 2 pages
@@ -158,7 +159,12 @@ void decode_kernel(DecParams p) {
   // a pass covers kPagesPerPass pages and a range kPasses passes.
   constexpr int kPagesPerPass = kDecThreads / G;
   constexpr int kPasses = (PACKED && G >= 4) ? 32 : 16;
-  constexpr int kRange = LOGICAL ? 2048 : kPagesPerPass * kPasses;   // 4096 / G pages (8192 / G packed, G >= 4)
+  // Phase A1 runs in halves of kPasses passes; a range of up to 2048 pages
+  // (two halves when one covers at most 1024) then has one compaction and one
+  // phase B.
+  constexpr int kHalf = kPagesPerPass * kPasses;
+  constexpr int kHalves = (!LOGICAL && kHalf <= 1024) ? 2 : 1;
+  constexpr int kRange = LOGICAL ? 2048 : kHalf * kHalves;
   constexpr int kPagesPerThread = kRange / kDecThreads;
   static_assert(!LOGICAL || kPagesPerThread == 8, "logical codes: 8 pages per thread");
   __shared__ int32_t page_phys[LOGICAL ? 1 : kRange];
@@ -350,13 +356,17 @@ void decode_kernel(DecParams p) {
         phj[j] = ph[j];
       }
     } else {
+    for (int hf = 0; hf < kHalves; ++hf) {
+    const int hb = r0 + hf * kHalf;                  // first page of this half
+    if (hb >= r1) break;
+    const bool pre = use_pre && hf == 0;             // the prologue fetched its block-table entries
     int phys[kPasses];
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps) {
-      if (use_pre) {
+      if (pre) {
         phys[ps] = phys0[ps];
       } else {
-        const int l = min(r0 + ps * kPagesPerPass + pslot, r1 - 1);
+        const int l = min(hb + ps * kPagesPerPass + pslot, r1 - 1);
         phys[ps] = p.bt[b * p.bts0 + l * p.bts1];
       }
     }
@@ -368,7 +378,7 @@ void decode_kernel(DecParams p) {
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
-        const bool need = !use_pre || ps * kPagesPerPass + pslot < r1;
+        const bool need = !pre || ps * kPagesPerPass + pslot < r1;
         cv[ps] = need ? p.codes[ph * p.cs0 + (h0 + gl) * p.cs1] : ~qcode;
       }
 #pragma unroll
@@ -379,7 +389,7 @@ void decode_kernel(DecParams p) {
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
-        const bool need = !use_pre || ps * kPagesPerPass + pslot < r1;
+        const bool need = !pre || ps * kPagesPerPass + pslot < r1;
         rv[ps] = need ? *reinterpret_cast<const int4*>(p.router + ph * p.rs0 + (h0 + gl) * p.rs1)
                       : int4{0, 0, 0, 0};
       }
@@ -397,7 +407,7 @@ void decode_kernel(DecParams p) {
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
         const int32_t* rv = p.router + ph * p.rs0 + (h0 + gl) * p.rs1;
-        bool ok = !use_pre || ps * kPagesPerPass + pslot < r1;
+        bool ok = !pre || ps * kPagesPerPass + pslot < r1;
         for (int lev = 0; ok && lev < p.r; ++lev) {
           if (rv[lev * p.rs2] != qroute[gl][lev]) {
             ok = false;
@@ -410,16 +420,17 @@ void decode_kernel(DecParams p) {
     }
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps) {
-      const int l = r0 + ps * kPagesPerPass + pslot;
+      const int l = hb + ps * kPagesPerPass + pslot;
       const bool valid = l < r1 && phys[ps] >= 0 && phys[ps] < p.P;
       const bool forced = (p.sink && l == 0) || (p.local > 0 && l >= n - p.local);
       const uint64_t bal = __ballot(valid && (forced || hit[ps]));
       if (gl == 0) {
         const int m = static_cast<int>((bal >> (lane - gl)) & ((1u << G) - 1u));
-        page_mask[ps * kPagesPerPass + pslot] = static_cast<uint8_t>(m);
-        page_phys[ps * kPagesPerPass + pslot] = phys[ps];
+        page_mask[hf * kHalf + ps * kPagesPerPass + pslot] = static_cast<uint8_t>(m);
+        page_phys[hf * kHalf + ps * kPagesPerPass + pslot] = phys[ps];
       }
     }
+    }   // halves
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kPagesPerThread; ++j) {
