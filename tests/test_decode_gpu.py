@@ -161,3 +161,17 @@ def test_config4_subset_and_properties():
     out2 = ultrametric_decode(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.router,
                               w.q_router, **kw)
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_range_and_half_boundaries(dtype):
+    # phase A runs 1024-page halves of 2048-page ranges at G = 4: sequences of
+    # 1024 / 1025 / 2047 / 2048 / 2049 pages end a half, start one, fill a range
+    # or spill into the next
+    page = 16
+    lens = [1024 * page, 1024 * page + 1, 2047 * page, 2048 * page, 2048 * page + 5]
+    args = make(B=5, H=8, Hkv=2, D=64, page=page, pages=2100, TD=4, p=2, lens=lens, dtype=dtype, seed=77)
+    for kw in (dict(req_depth=3, local_blocks=2, sink_block=True), dict(req_depth=4)):
+        out = run(args, **kw)
+        ref = oracle(args, dtype, **kw)
+        assert np.abs(out.float().cpu().numpy() - ref).max() <= TOL[dtype], kw
