@@ -195,7 +195,23 @@ void decode_kernel(DecParams p) {
   // range's block-table entries (split 0 starts at page 0 whatever the
   // context length), the context length, the query routing vectors and Q.
   const bool prefetched = split == 0 && p.max_pages > 0;
-  int phys0[LOGICAL ? 1 : kPasses];
+  // Block-table entries of pages lb .. lb + kPagesPerThread - 1 (clamped to
+  // the table; 16-byte reads when the row is contiguous and aligned).
+  auto load_bt = [&](int lb, int (&ph)[kPagesPerThread]) {
+    if (kPagesPerThread % 4 == 0 && p.bts1 == 1 && (p.bts0 & 3) == 0 &&
+        (reinterpret_cast<uintptr_t>(p.bt) & 15) == 0 && lb + kPagesPerThread <= p.max_pages) {
+      const int4* src = reinterpret_cast<const int4*>(p.bt + static_cast<int64_t>(b) * p.bts0 + lb);
+#pragma unroll
+      for (int c = 0; c < kPagesPerThread / 4; ++c) {
+        const int4 u = src[c];
+        ph[4 * c] = u.x; ph[4 * c + 1] = u.y; ph[4 * c + 2] = u.z; ph[4 * c + 3] = u.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kPagesPerThread; ++j) ph[j] = p.bt[b * p.bts0 + min(lb + j, p.max_pages - 1) * p.bts1];
+    }
+  };
+  int phys0[LOGICAL ? 1 : kPagesPerThread];
   // Logical codes: block-table entries and the G heads' codes of pages
   // lb .. lb + 7 (indices clamped to the table; results past the range are
   // discarded).
@@ -254,11 +270,7 @@ void decode_kernel(DecParams p) {
     if constexpr (LOGICAL) {
       load_logical(8 * tid, lcw0, lph0);
     } else {
-#pragma unroll
-      for (int ps = 0; ps < kPasses; ++ps) {
-        const int l = min(ps * kPagesPerPass + pslot, p.max_pages - 1);
-        phys0[ps] = p.bt[b * p.bts0 + l * p.bts1];
-      }
+      load_bt(kPagesPerThread * tid, phys0);
     }
   }
   const int ctx = p.ctx[b];
@@ -299,6 +311,12 @@ void decode_kernel(DecParams p) {
     for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
     m_s[g] = -INFINITY;
     l_s[g] = 0.f;
+  }
+  if constexpr (!LOGICAL) {
+    if (prefetched) {
+#pragma unroll
+      for (int j = 0; j < kPagesPerThread; ++j) page_phys[kPagesPerThread * tid + j] = phys0[j];
+    }
   }
   if constexpr (!PACKED && !LOGICAL) {   // the code modes carry no level-wise query router
     for (int i = tid; i < G * p.r; i += kDecThreads) {
@@ -356,20 +374,20 @@ void decode_kernel(DecParams p) {
         phj[j] = ph[j];
       }
     } else {
+    if (!use_pre) {
+      // the range's block-table entries into LDS (the prologue did the first range's)
+      int ph[kPagesPerThread];
+      load_bt(r0 + kPagesPerThread * tid, ph);
+#pragma unroll
+      for (int j = 0; j < kPagesPerThread; ++j) page_phys[kPagesPerThread * tid + j] = ph[j];
+      __syncthreads();
+    }
     for (int hf = 0; hf < kHalves; ++hf) {
     const int hb = r0 + hf * kHalf;                  // first page of this half
     if (hb >= r1) break;
-    const bool pre = use_pre && hf == 0;             // the prologue fetched its block-table entries
     int phys[kPasses];
 #pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-      if (pre) {
-        phys[ps] = phys0[ps];
-      } else {
-        const int l = min(hb + ps * kPagesPerPass + pslot, r1 - 1);
-        phys[ps] = p.bt[b * p.bts0 + l * p.bts1];
-      }
-    }
+    for (int ps = 0; ps < kPasses; ++ps) phys[ps] = page_phys[hf * kHalf + ps * kPagesPerPass + pslot];
     bool hit[kPasses];
     if constexpr (PACKED) {
       // Packed codes: one 32-bit word per (page, head); the first r levels
@@ -378,7 +396,7 @@ void decode_kernel(DecParams p) {
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
-        const bool need = !pre || ps * kPagesPerPass + pslot < r1;
+        const bool need = hb + ps * kPagesPerPass + pslot < r1;
         cv[ps] = need ? p.codes[ph * p.cs0 + (h0 + gl) * p.cs1] : ~qcode;
       }
 #pragma unroll
@@ -389,7 +407,7 @@ void decode_kernel(DecParams p) {
 #pragma unroll
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
-        const bool need = !pre || ps * kPagesPerPass + pslot < r1;
+        const bool need = hb + ps * kPagesPerPass + pslot < r1;
         rv[ps] = need ? *reinterpret_cast<const int4*>(p.router + ph * p.rs0 + (h0 + gl) * p.rs1)
                       : int4{0, 0, 0, 0};
       }
@@ -407,7 +425,7 @@ void decode_kernel(DecParams p) {
       for (int ps = 0; ps < kPasses; ++ps) {
         const int ph = (phys[ps] >= 0 && phys[ps] < p.P) ? phys[ps] : 0;
         const int32_t* rv = p.router + ph * p.rs0 + (h0 + gl) * p.rs1;
-        bool ok = !pre || ps * kPagesPerPass + pslot < r1;
+        bool ok = hb + ps * kPagesPerPass + pslot < r1;
         for (int lev = 0; ok && lev < p.r; ++lev) {
           if (rv[lev * p.rs2] != qroute[gl][lev]) {
             ok = false;
@@ -427,7 +445,6 @@ void decode_kernel(DecParams p) {
       if (gl == 0) {
         const int m = static_cast<int>((bal >> (lane - gl)) & ((1u << G) - 1u));
         page_mask[hf * kHalf + ps * kPagesPerPass + pslot] = static_cast<uint8_t>(m);
-        page_phys[hf * kHalf + ps * kPagesPerPass + pslot] = phys[ps];
       }
     }
     }   // halves
