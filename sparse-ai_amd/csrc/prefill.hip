@@ -16,7 +16,7 @@
 //    tile: row max / row sum need one exchange with lane ^ 32
 //    (permlane32_swap), and the O^T = V^T P^T accumulator is rescaled with a
 //    per-lane scalar, lazily (only when a row max grows by more than 2^8).
-//    K/V tiles of BN = 32 keys stream through a 4-stage LDS ring filled by
+//    K/V tiles of BN = 32 keys stream through a 3-stage LDS ring filled by
 //    direct-to-LDS loads (global_load_lds_dwordx4, no VGPR staging); rows
 //    are stored with an XOR swizzle on 16-byte chunks, K is read as
 //    row-major 16-byte MFMA operands and V through ds_read_b64_tr_b16
