@@ -114,7 +114,8 @@ def block_sparse_attention_ref(q: np.ndarray, k: np.ndarray, v: np.ndarray, bloc
 def block_sparse_attention_grad_ref(q: np.ndarray, k: np.ndarray, v: np.ndarray, block_mask: np.ndarray,
                                     route_block: int, dout: np.ndarray, *, is_causal: bool = False,
                                     sm_scale: Optional[float] = None,
-                                    pair_bias: Optional[np.ndarray] = None):
+                                    pair_bias: Optional[np.ndarray] = None,
+                                    out: Optional[np.ndarray] = None):
     """Gradients of ``block_sparse_attention_ref``'s output, float64
     (the analytic backward of block_list.py:494-681,758-880):
     with P = softmax(S) over the visible columns of a row,
@@ -124,6 +125,12 @@ def block_sparse_attention_grad_ref(q: np.ndarray, k: np.ndarray, v: np.ndarray,
     the pair. k / v may carry H_kv | H heads (their gradients sum over the
     query heads that read them).
     Returns (dq, dk, dv, d_pair_bias (Z, H, NB, NB)) as float64.
+    ``out``: the forward output as the forward stored it (e.g. rounded to
+    bf16). When given, delta = rowsum(dO * out) is taken from it, as the
+    reference's backward does (block_list.py:784-785); otherwise from the
+    exact float64 output. The two differ by the output's rounding, which
+    matters for sums of dS that cancel exactly (a bias gradient over a row
+    whose visible keys all lie in one block is 0 with the exact output).
     """
     Z, H, N, D = q.shape
     Hkv = k.shape[1]
@@ -165,7 +172,7 @@ def block_sparse_attention_grad_ref(q: np.ndarray, k: np.ndarray, v: np.ndarray,
                 den = e.sum(-1, keepdims=True)
                 pm = np.where(den > 0, e / np.where(den > 0, den, 1.0), 0.0)
                 do = dout[z, h, r0:r1].astype(np.float64)
-                o = pm @ vf[cols]
+                o = pm @ vf[cols] if out is None else out[z, h, r0:r1].astype(np.float64)
                 dp = do @ vf[cols].T
                 ds = pm * (dp - (do * o).sum(-1, keepdims=True))
                 dq[z, h, r0:r1] += scale * ds @ kf[cols]

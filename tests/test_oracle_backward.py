@@ -75,3 +75,28 @@ def test_grad_ref_finite_differences():
             lm = loss(q, k, v, pb)
             arr[idx] = a0
             assert abs((lp - lm) / (2 * eps) - grad[idx]) < 1e-6, idx
+
+
+def test_grad_ref_delta_from_stored_output():
+    # `out` replaces the exact output in delta = rowsum(dO * out) (block_list.py:784-785).
+    # With the exact output it changes nothing. With a perturbed one, sum_j dS_ij =
+    # dO_i . O_i - delta_i = dO_i . (O_i - out_i): the bias gradient of a pair that holds
+    # all of a row's visible keys (here: one block per row) is that sum over its rows.
+    rng = np.random.default_rng(11)
+    Z, H, N, D, rb = 1, 2, 24, 8, 8
+    q, k, v, dout = (rng.standard_normal((Z, H, N, D)) for _ in range(4))
+    NB = N // rb
+    bm = np.broadcast_to(np.eye(NB, dtype=bool), (Z, H, NB, NB)).copy()
+    o, _ = oa.block_sparse_attention_ref(q, k, v, bm, rb, is_causal=True)
+    base = oa.block_sparse_attention_grad_ref(q, k, v, bm, rb, dout, is_causal=True)
+    same = oa.block_sparse_attention_grad_ref(q, k, v, bm, rb, dout, is_causal=True, out=o)
+    for a, b in zip(base, same):
+        assert np.allclose(a, b, rtol=0, atol=1e-12)
+    assert np.abs(base[3]).max() < 1e-12
+    stored = o + rng.standard_normal(o.shape) * 1e-3
+    dpb = oa.block_sparse_attention_grad_ref(q, k, v, bm, rb, dout, is_causal=True, out=stored)[3]
+    for h in range(H):
+        for qb in range(NB):
+            r = slice(qb * rb, (qb + 1) * rb)
+            want = float((dout[0, h, r] * (o[0, h, r] - stored[0, h, r])).sum())
+            assert abs(dpb[0, h, qb, qb] - want) < 1e-12

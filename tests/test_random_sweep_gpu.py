@@ -1,0 +1,194 @@
+"""GPU parity over seeded random combinations of the features that the grid
+tests cover one at a time: prefill with GQA, soft block bias, LSE, per-head
+routing depths, ragged sequence lengths, every route block and head dim the
+kernels take, causal / sink / local masks, and strided inputs; the backward on
+the same kind of cases; decode with random page sizes, group sizes, depths,
+ragged and empty contexts, through the int32 router and the packed-code
+entry. Every case checks against the float64 oracle (fp32 1e-5, bf16 2e-2,
+fp16 2e-3 on outputs; gradients relative to their largest entry). The case
+parameters are drawn from a fixed seed, so the set is the same on every run
+and a failure names its case."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import blocks as ob
+from oracle import decode as od
+from ultrametric import block_list_attention, build_block_lists, ultrametric_decode
+from ultrametric.kernel_decode import pack_routing_codes, ultrametric_decode_packed
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-3}
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def _fwd_cases(n):
+    rng = np.random.default_rng(2024)
+    cases = []
+    for i in range(n):
+        rb = int(rng.choice([16, 32, 64, 128]))
+        D = int(rng.choice([16, 32, 64, 128, 256]))
+        Hkv = int(rng.choice([1, 2]))
+        G = int(rng.choice([1, 2, 4]))
+        N = int(rng.integers(1, 6 * rb + 1))
+        cases.append(dict(i=i, dtype=DTYPES[int(rng.integers(0, 3))], rb=rb, D=D, Z=int(rng.integers(1, 3)),
+                          H=Hkv * G, Hkv=Hkv, N=N, TD=int(rng.integers(1, 5)), p=int(rng.integers(2, 4)),
+                          causal=bool(rng.integers(0, 2)), sink=bool(rng.integers(0, 2)),
+                          local=int(rng.integers(0, 3)), bias=bool(rng.integers(0, 2)),
+                          strided=bool(rng.integers(0, 2)), seed=int(rng.integers(0, 1 << 30))))
+    return cases
+
+
+def _case_id(c):
+    return f"{c['i']}-{str(c['dtype'])[6:]}-rb{c['rb']}-D{c['D']}-H{c['H']}/{c['Hkv']}-N{c['N']}"
+
+
+def _inputs(c):
+    g = torch.Generator().manual_seed(c["seed"])
+    Z, H, Hkv, N, D = c["Z"], c["H"], c["Hkv"], c["N"], c["D"]
+    q = torch.randn(Z, H, N, D, generator=g).to(c["dtype"])
+    k = torch.randn(Z, Hkv, N, D, generator=g).to(c["dtype"])
+    v = torch.randn(Z, Hkv, N, D, generator=g).to(c["dtype"])
+    NB = -(-N // c["rb"])
+    router = torch.randint(0, c["p"], (Z, H, NB, c["TD"]), generator=g, dtype=torch.int32)
+    depth = torch.randint(0, c["TD"] + 1, (H,), generator=g)
+    return q, k, v, router, depth, g
+
+
+def _device(t, strided):
+    if not strided:
+        return t.to(DEV)
+    # (Z, N, H, D) storage viewed as (Z, H, N, D)
+    return t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+
+
+def _reference(c, q, k, v, bl, bias, grad=False, dout=None, out=None):
+    lists, counts = bl.lists.cpu().numpy(), bl.counts.cpu().numpy()
+    bm = ob.lists_to_mask(lists, counts, counts.shape[-1])
+    pair_bias = None
+    if bias is not None:
+        pair_bias = np.zeros(bm.shape)
+        for z, h, qb in np.ndindex(counts.shape):
+            for t in range(counts[z, h, qb]):
+                pair_bias[z, h, qb, lists[z, h, qb, t]] = bias[z, h, qb, t].item()
+    # k / v keep their H_kv heads: the oracle maps query head h to kv head h // (H / H_kv)
+    qf, kf, vf = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    if not grad:
+        return oa.block_sparse_attention_ref(qf, kf, vf, bm, c["rb"], is_causal=c["causal"], pair_bias=pair_bias)
+    return oa.block_sparse_attention_grad_ref(qf, kf, vf, bm, c["rb"], dout.float().numpy(),
+                                              is_causal=c["causal"], pair_bias=pair_bias, out=out)
+
+
+@pytest.mark.parametrize("c", _fwd_cases(96), ids=_case_id)
+def test_forward_random_combination(c):
+    q, k, v, router, depth, g = _inputs(c)
+    kw = dict(is_causal=c["causal"], sink_block=c["sink"], local_blocks=c["local"])
+    bl = build_block_lists(router.to(DEV), depth.to(DEV), **kw)
+    # the lists themselves: bit-exact against the oracle's builder
+    ref_bl = ob.build_block_lists(router.numpy(), depth.numpy(), **kw)
+    assert np.array_equal(bl.counts.cpu().numpy(), ref_bl.counts)
+    got_l = bl.lists.cpu().numpy()
+    for z, h, qb in np.ndindex(ref_bl.counts.shape):
+        n = ref_bl.counts[z, h, qb]
+        assert np.array_equal(got_l[z, h, qb, :n], ref_bl.lists[z, h, qb, :n])
+    bias = torch.randn(*bl.counts.shape, bl.max_count, generator=g) if c["bias"] and bl.max_count > 0 else None
+    out, lse = block_list_attention(_device(q, c["strided"]), _device(k, c["strided"]), _device(v, c["strided"]),
+                                    bl, route_block=c["rb"], is_causal=c["causal"], return_lse=True,
+                                    soft_block_bias=None if bias is None else bias.to(DEV))
+    ref, ref_lse = _reference(c, q, k, v, bl, bias)
+    err = np.abs(out.float().cpu().numpy() - ref).max() if ref.size else 0.0
+    assert err <= TOL[c["dtype"]], err
+    l = lse.cpu().numpy().astype(np.float64)
+    assert np.array_equal(np.isneginf(l), np.isneginf(ref_lse))
+    fin = ~np.isneginf(ref_lse)
+    if fin.any():
+        assert np.abs(l[fin] - ref_lse[fin]).max() <= max(TOL[c["dtype"]], 1e-5) * 2
+
+
+def _bwd_cases(n):
+    cs = [c for c in _fwd_cases(240) if c["D"] in (32, 64, 128) and c["N"] <= 400]
+    rng = np.random.default_rng(7)
+    for c in cs:
+        c["dtype"] = DTYPES[int(rng.integers(0, 3))]
+    return cs[:n]
+
+
+@pytest.mark.parametrize("c", _bwd_cases(32), ids=_case_id)
+def test_backward_random_combination(c):
+    q, k, v, router, depth, g = _inputs(c)
+    kw = dict(is_causal=c["causal"], sink_block=c["sink"], local_blocks=c["local"])
+    bl = build_block_lists(router.to(DEV), depth.to(DEV), **kw)
+    bias = torch.randn(*bl.counts.shape, bl.max_count, generator=g) if c["bias"] and bl.max_count > 0 else None
+    dout = torch.randn(q.shape, generator=g).to(c["dtype"])
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    bd = bias.to(DEV).requires_grad_(True) if bias is not None else None
+    out = block_list_attention(qd, kd, vd, bl, route_block=c["rb"], is_causal=c["causal"], soft_block_bias=bd)
+    out.backward(dout.to(DEV))
+    # delta from the stored forward output, as the reference's backward takes it
+    # (block_list.py:784-785); the output itself is checked by the forward cases
+    rdq, rdk, rdv, rdpair = _reference(c, q, k, v, bl, bias, grad=True, dout=dout,
+                                       out=out.detach().float().cpu().numpy())
+    want = {"dq": rdq, "dk": rdk, "dv": rdv}
+    got = {"dq": qd.grad, "dk": kd.grad, "dv": vd.grad}
+    # relative to the gradient's largest entry, floored at 1 (gradients here are O(1))
+    rel = 1e-4 if c["dtype"] == torch.float32 else 2e-2
+    for name in want:
+        w = want[name]
+        scale = max(np.abs(w).max(), 1.0)
+        err = np.abs(got[name].float().cpu().numpy() - w).max() / scale
+        assert err <= rel, (name, err)
+    if bd is not None:
+        w = np.zeros(bias.shape)
+        lists, counts = bl.lists.cpu().numpy(), bl.counts.cpu().numpy()
+        for z, h, qb in np.ndindex(counts.shape):
+            for t in range(counts[z, h, qb]):
+                w[z, h, qb, t] = rdpair[z, h, qb, lists[z, h, qb, t]]
+        scale = max(np.abs(w).max(), 1.0)
+        assert np.abs(bd.grad.float().cpu().numpy() - w).max() / scale <= rel
+
+
+def _dec_cases(n):
+    rng = np.random.default_rng(99)
+    cases = []
+    for i in range(n):
+        page = int(rng.choice([8, 16, 32]))
+        G = int(rng.choice([1, 2, 4, 8]))
+        Hkv = int(rng.choice([1, 2, 4]))
+        B = int(rng.integers(1, 7))
+        lens = [int(rng.choice([0, 1, int(rng.integers(1, 40 * page))])) for _ in range(B)]
+        cases.append(dict(i=i, dtype=DTYPES[int(rng.integers(0, 3))], page=page, H=Hkv * G, Hkv=Hkv,
+                          D=int(rng.choice([64, 128])), B=B, lens=lens, TD=int(rng.integers(1, 5)),
+                          depth=int(rng.integers(0, 6)), local=int(rng.integers(0, 3)),
+                          sink=bool(rng.integers(0, 2)), seed=int(rng.integers(0, 1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("c", _dec_cases(48),
+                         ids=lambda c: f"{c['i']}-{str(c['dtype'])[6:]}-pg{c['page']}-H{c['H']}/{c['Hkv']}-D{c['D']}")
+def test_decode_random_combination(c):
+    g = torch.Generator().manual_seed(c["seed"])
+    B, H, Hkv, D, page, TD = c["B"], c["H"], c["Hkv"], c["D"], c["page"], c["TD"]
+    mp = max(1, max(-(-l // page) for l in c["lens"]))
+    pages = mp + 7
+    q = torch.randn(B, H, D, generator=g).to(c["dtype"])
+    kc = torch.randn(pages, Hkv, page, D, generator=g).to(c["dtype"])
+    vc = torch.randn(pages, Hkv, page, D, generator=g).to(c["dtype"])
+    bt = torch.stack([torch.randperm(pages, generator=g)[:mp] for _ in range(B)]).to(torch.int32)
+    ctx = torch.tensor(c["lens"], dtype=torch.int32)
+    r = torch.randint(0, 2, (pages, H, TD), generator=g, dtype=torch.int32)
+    qr = torch.randint(0, 2, (B, H, TD), generator=g, dtype=torch.int32)
+    kw = dict(req_depth=c["depth"], local_blocks=c["local"], sink_block=c["sink"])
+    out = ultrametric_decode(*(t.to(DEV) for t in (q, kc, vc, bt, ctx, r, qr)), **kw)
+    ref = od.decode_reference(q.float().numpy(), kc.float().numpy(), vc.float().numpy(), bt.numpy(), ctx.numpy(),
+                              r.numpy(), qr.numpy(), **kw)
+    err = np.abs(out.float().cpu().numpy() - ref).max()
+    assert err <= TOL[c["dtype"]], err
+    # packed codes (1 bit per level): the same pages, the same numbers
+    pc, qc = pack_routing_codes(r.to(DEV), 1), pack_routing_codes(qr.to(DEV), 1)
+    outp = ultrametric_decode_packed(*(t.to(DEV) for t in (q, kc, vc, bt, ctx)), pc, qc, TD, 1, **kw)
+    assert torch.equal(outp, out)
