@@ -4,7 +4,7 @@ routing depths, ragged sequence lengths, every route block and head dim the
 kernels take, causal / sink / local masks, and strided inputs; the backward on
 the same kind of cases; decode with random page sizes, group sizes, depths,
 ragged and empty contexts, through the int32 router and the packed-code
-entry. Every case checks against the float64 oracle (fp32 1e-5, bf16 2e-2,
+entry; the fused routed prefill against the two-launch path. Every case checks against the float64 oracle (fp32 1e-5, bf16 2e-2,
 fp16 2e-3 on outputs; gradients relative to their largest entry). The case
 parameters are drawn from a fixed seed, so the set is the same on every run
 and a failure names its case."""
@@ -192,3 +192,35 @@ def test_decode_random_combination(c):
     pc, qc = pack_routing_codes(r.to(DEV), 1), pack_routing_codes(qr.to(DEV), 1)
     outp = ultrametric_decode_packed(*(t.to(DEV) for t in (q, kc, vc, bt, ctx)), pc, qc, TD, 1, **kw)
     assert torch.equal(outp, out)
+
+
+def _fused_cases(n):
+    rng = np.random.default_rng(31)
+    cases = []
+    for i in range(n):
+        rb = int(rng.choice([32, 64, 128]))
+        Hkv = int(rng.choice([1, 2]))
+        cases.append(dict(i=i, dtype=[torch.bfloat16, torch.float16][int(rng.integers(0, 2))], rb=rb,
+                          D=int(rng.choice([32, 64, 128])), Z=int(rng.integers(1, 3)),
+                          H=Hkv * int(rng.choice([1, 2, 4])), Hkv=Hkv, N=int(rng.integers(1, 12 * rb + 1)),
+                          TD=int(rng.integers(1, 5)), p=int(rng.integers(2, 5)),
+                          causal=bool(rng.integers(0, 2)), sink=bool(rng.integers(0, 2)),
+                          local=int(rng.integers(0, 3)), seed=int(rng.integers(0, 1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("c", _fused_cases(32), ids=_case_id)
+def test_fused_routed_random_combination(c):
+    # the one-launch routed prefill (list build inside the forward kernel) against
+    # the two-launch path: lists, counts and output identical bit for bit
+    from ultrametric.block_list import _routed_fused
+    q, k, v, router, depth, _ = _inputs(c)
+    qd, kd, vd, rd = (t.to(DEV) for t in (q, k, v, router))
+    kw = dict(is_causal=c["causal"], sink_block=c["sink"], local_blocks=c["local"])
+    fused = _routed_fused(qd, kd, vd, rd, depth, route_block=c["rb"], sm_scale=None, arity=c["p"], **kw)
+    assert fused is not None
+    out, bl_f = fused
+    bl = build_block_lists(rd, depth, arity=c["p"], **kw)
+    assert torch.equal(bl_f.counts, bl.counts)
+    assert torch.equal(bl_f.lists, bl.lists)
+    assert torch.equal(out, block_list_attention(qd, kd, vd, bl, route_block=c["rb"], is_causal=c["causal"]))
