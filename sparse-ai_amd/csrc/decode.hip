@@ -198,7 +198,7 @@ void decode_kernel(DecParams p) {
   // Block-table entries of pages lb .. lb + kPagesPerThread - 1 (clamped to
   // the table; 16-byte reads when the row is contiguous and aligned).
   auto load_bt = [&](int lb, int (&ph)[kPagesPerThread]) {
-    if (kPagesPerThread % 4 == 0 && p.bts1 == 1 && (p.bts0 & 3) == 0 &&
+    if (kPagesPerThread % 4 == 0 && p.bts1 == 1 && (p.bts0 & 3) == 0 && (lb & 3) == 0 &&
         (reinterpret_cast<uintptr_t>(p.bt) & 15) == 0 && lb + kPagesPerThread <= p.max_pages) {
       const int4* src = reinterpret_cast<const int4*>(p.bt + static_cast<int64_t>(b) * p.bts0 + lb);
 #pragma unroll
@@ -216,7 +216,7 @@ void decode_kernel(DecParams p) {
   // lb .. lb + 7 (indices clamped to the table; results past the range are
   // discarded).
   auto load_logical = [&](int lb, uint32_t (&cw)[G][8], int (&ph)[8]) {
-    if (p.bts1 == 1 && (p.bts0 & 3) == 0 && (reinterpret_cast<uintptr_t>(p.bt) & 15) == 0 &&
+    if (p.bts1 == 1 && (p.bts0 & 3) == 0 && (lb & 3) == 0 && (reinterpret_cast<uintptr_t>(p.bt) & 15) == 0 &&
         lb + 8 <= p.max_pages) {
       // 8 consecutive entries, 16-byte aligned: two 16-byte reads
       const int4* src = reinterpret_cast<const int4*>(p.bt + static_cast<int64_t>(b) * p.bts0 + lb);
@@ -228,7 +228,7 @@ void decode_kernel(DecParams p) {
       for (int j = 0; j < 8; ++j) ph[j] = p.bt[b * p.bts0 + min(lb + j, p.max_pages - 1) * p.bts1];
     }
     const char* cb = static_cast<const char*>(p.lcodes);
-    if (p.lvec && lb + 8 <= p.max_pages) {
+    if (p.lvec && (lb & 7) == 0 && lb + 8 <= p.max_pages) {
       // 8 consecutive codes: one 8-, 16- or 32-byte read per head
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -276,9 +276,12 @@ void decode_kernel(DecParams p) {
   const int ctx = p.ctx[b];
   int n = ctx > 0 ? (ctx + p.PS - 1) / p.PS : 0;
   if (n > p.max_pages) n = p.max_pages;  // block-table bound (memory safety)
-  // This split's logical page range [pa, pz).
-  const int pa = static_cast<int>((static_cast<long long>(n) * split) / p.splits);
-  const int pz = static_cast<int>((static_cast<long long>(n) * (split + 1)) / p.splits);
+  // This split's logical page range [pa, pz). Split boundaries are rounded
+  // down to multiples of 8 pages, so that every range starts 16-byte aligned
+  // in the block table and the code arrays (the vector reads below).
+  const int pa = static_cast<int>((static_cast<long long>(n) * split) / p.splits) & ~7;
+  const int pz = split + 1 == p.splits ? n
+                                       : static_cast<int>((static_cast<long long>(n) * (split + 1)) / p.splits) & ~7;
 
   const int grp = lane >> 4, sub = lane & 15;
   constexpr int QW = RowRegs<T, DPL>::kWords;

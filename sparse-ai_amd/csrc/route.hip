@@ -49,6 +49,12 @@ __device__ __forceinline__ void load4(const T* src, float (&x)[4]) {
   }
 }
 
+// Argmax order of torch.argmax: the first maximum wins ties, and a NaN counts
+// as the maximum (the first NaN wins).
+__device__ __forceinline__ bool beats(float y, float best) {
+  return y > best || (y != y && best == best);
+}
+
 template <typename T>
 __global__ __launch_bounds__(kVoteThreads) void route_vote_kernel(VoteParams p) {
   __shared__ int votes[kMaxR][kMaxP];
@@ -75,13 +81,13 @@ __global__ __launch_bounds__(kVoteThreads) void route_vote_kernel(VoteParams p) 
       load4<T>(row, x);
 #pragma unroll
       for (int c = 1; c < 4; ++c) {
-        if (x[c] > x[arg]) arg = c;   // first maximum wins ties
+        if (beats(x[c], x[arg])) arg = c;
       }
     } else {
       float best = Elem<T>::load(row);
       for (int c = 1; c < p.P; ++c) {
         const float y = Elem<T>::load(row + c * p.s4);
-        if (y > best) {   // first maximum wins ties
+        if (beats(y, best)) {
           best = y;
           arg = c;
         }

@@ -23,8 +23,14 @@ formulations (block_list.py:334-378) for callers' correctness checks; no
 function above calls them.
 
 There is no CPU fallback: CPU tensors or a missing library raise RuntimeError.
-Backward (the reference's sparse autograd, block_list.py:494-961) is not
-implemented here yet; a forward that needs grad raises RuntimeError.
+
+``block_list_attention`` is differentiable in q, k, v and ``soft_block_bias``
+(the reference's sparse autograd, block_list.py:494-961): the backward
+computes delta = rowsum(dO * O) inside the dQ kernel, which walks each query
+tile's list; dK and dV walk each key tile's transposed list; the soft-bias
+gradient of a (query block, list slot) is the sum of dS over that pair. The
+one host read of the backward is the work plan's three counts, at the point
+where the reference reads max(q_counts) (block_list.py:320).
 """
 
 from __future__ import annotations

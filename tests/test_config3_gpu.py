@@ -1,8 +1,11 @@
 """GPU parity on BASELINE config 3 (bf16, H32, D128, causal, route block 128,
 per-head Bernoulli(rho) lower-triangular block masks + diagonal + sink):
-exact against the float64 oracle on a subset of heads at N = 2048 for each
-density, and at N = 32768 through size-independent properties (causal query 0
-sees only key 0, so its output is V's first row exactly; determinism)."""
+exact against the float64 oracle on a subset of heads at N = 2048 and
+N = 8192 for each density, and at N = 32768 through size-independent
+properties (causal query 0 sees only key 0, so its output is V's first row
+exactly; determinism) for rho in {1, 0.25, 0.016}. At rho = 1 the last query
+block lists all 256 key blocks, exactly one 256-entry list segment of the
+kernel: its rows are also checked against the oracle on two heads."""
 
 import math
 
@@ -34,7 +37,23 @@ def test_config3_n2048_heads_exact(rho):
         assert np.abs(l[z, h] - ref_lse[z, h]).max() <= 2e-2, (rho, h)
 
 
-@pytest.mark.parametrize("rho", [0.25, 0.016])
+@pytest.mark.parametrize("rho", [1.0, 0.5, 0.25, 0.0625, 0.016])
+def test_config3_n8192_heads_exact(rho):
+    c = wl.config3(8192, rho, device="cpu")
+    q, k, v, mask = c["q"], c["k"], c["v"], c["block_mask"]
+    bl = block_lists_from_mask(mask.to(DEV), is_causal=True)
+    out, lse = block_list_attention(q.to(DEV), k.to(DEV), v.to(DEV), bl, route_block=128, is_causal=True,
+                                    return_lse=True)
+    heads = [(0, 3), (0, 20), (0, 30)]
+    ref, ref_lse = oa.block_sparse_attention_ref(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                                 mask.numpy(), 128, is_causal=True, heads=heads)
+    o, l = out.float().cpu().numpy(), lse.cpu().numpy()
+    for z, h in heads:
+        assert np.abs(o[z, h] - ref[z, h]).max() <= 2e-2, (rho, h)
+        assert np.abs(l[z, h] - ref_lse[z, h]).max() <= 2e-2, (rho, h)
+
+
+@pytest.mark.parametrize("rho", [1.0, 0.25, 0.016])
 def test_config3_n32768_properties(rho):
     Z, H, N, D, RB = 1, 32, 32768, 128, 128
     g = torch.Generator(device=DEV).manual_seed(33)
@@ -46,3 +65,13 @@ def test_config3_n32768_properties(rho):
     assert torch.equal(out[:, :, 0], v[:, :, 0])          # query 0 attends key 0 only
     out2 = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True, sm_scale=1.0 / math.sqrt(D))
     assert torch.equal(out, out2)
+    if rho == 1.0:
+        # the last query block lists every key block: 256 entries, one full list segment
+        assert int(bl.counts[0, 0, -1]) == N // RB
+        qh, kh, vh, oh = (t[0].float().cpu().numpy() for t in (q, k, v, out))
+        rows = np.arange(N - RB, N)
+        for h in (0, 31):
+            m = rows[:, None] >= np.arange(N)[None, :]
+            ref, _ = oa._rows_attention(qh[h, rows].astype(np.float64), kh[h].astype(np.float64),
+                                        vh[h].astype(np.float64), m, 1.0 / math.sqrt(D))
+            assert np.abs(oh[h, rows] - ref).max() <= 2e-2, h

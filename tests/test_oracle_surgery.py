@@ -73,3 +73,16 @@ def test_allowed_key_stats_match_token_mask(S, rb, lw, r):
     assert st["mean_causal_keys"] == (S + 1) / 2
     NB = -(-S // rb)
     assert abs(st["block_density"] - mask.sum() / (2 * NB * (NB + 1) / 2)) < 1e-12
+
+
+def test_majority_route_nan_scores_match_torch_chain():
+    # the reference's chain: argmax (first NaN wins) -> one-hot -> sum over the block -> argmax
+    import torch
+    g = torch.Generator().manual_seed(4)
+    a = torch.randn(1, 2, 40, 2, 3, generator=g)
+    a = a.masked_fill(torch.rand(a.shape, generator=g) < 0.2, float("nan"))
+    rb = 8
+    idx = a.argmax(-1)
+    votes = torch.nn.functional.one_hot(idx, 3).float().view(1, 2, 5, rb, 2, 3).sum(3)
+    ref = votes.argmax(-1).to(torch.int32).numpy()
+    assert np.array_equal(osg.majority_route(a.numpy(), 2, rb), ref)

@@ -4,8 +4,10 @@ routing depths, ragged sequence lengths, every route block and head dim the
 kernels take, causal / sink / local masks, and strided inputs; the backward on
 the same kind of cases; decode with random page sizes, group sizes, depths,
 ragged and empty contexts, through the int32 router and the packed-code
-entry; the fused routed prefill against the two-launch path. Every case checks against the float64 oracle (fp32 1e-5, bf16 2e-2,
-fp16 2e-3 on outputs; gradients relative to their largest entry). The case
+entry; the fused routed prefill (list build inside the forward kernel), bit
+for bit against the two-launch path. Every case, the fused ones included,
+checks against the float64 oracle (fp32 1e-5, bf16 2e-2, fp16 2e-3 on
+outputs; gradients relative to their largest entry; lists bit-exact). The case
 parameters are drawn from a fixed seed, so the set is the same on every run
 and a failure names its case."""
 
@@ -224,3 +226,13 @@ def test_fused_routed_random_combination(c):
     assert torch.equal(bl_f.counts, bl.counts)
     assert torch.equal(bl_f.lists, bl.lists)
     assert torch.equal(out, block_list_attention(qd, kd, vd, bl, route_block=c["rb"], is_causal=c["causal"]))
+    # and both against the oracle: lists bit-exact, output at the dtype's tolerance
+    ref_bl = ob.build_block_lists(router.numpy(), depth.numpy(), arity=c["p"], **kw)
+    assert np.array_equal(bl_f.counts.cpu().numpy(), ref_bl.counts)
+    got_l = bl_f.lists.cpu().numpy()
+    for z, h, qb in np.ndindex(ref_bl.counts.shape):
+        n = ref_bl.counts[z, h, qb]
+        assert np.array_equal(got_l[z, h, qb, :n], ref_bl.lists[z, h, qb, :n])
+    ref, _ = _reference(c, q, k, v, bl_f, None)
+    err = np.abs(out.float().cpu().numpy() - ref).max() if ref.size else 0.0
+    assert err <= TOL[c["dtype"]], err

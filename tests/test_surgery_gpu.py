@@ -47,6 +47,21 @@ def test_vote_ties_and_strided():
     assert np.array_equal(route_block_vote(view.to(DEV), 2, 1).cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_vote_nan_scores_follow_torch_argmax(dtype):
+    # torch.argmax (surgery.py:543) treats the first NaN of a token's scores as
+    # the maximum; the vote counts that branch.
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(1, 2, 96, 3, 4, generator=g)
+    nan = torch.rand(1, 2, 96, 3, 4, generator=g) < 0.15
+    a = a.masked_fill(nan, float("nan")).to(dtype)
+    ref = osg.majority_route(a.float().numpy(), 3, 16)
+    assert np.array_equal(route_block_vote(a.to(DEV), 3, 16).cpu().numpy(), ref)
+    # the strided (non-vector) path too
+    view = a.float().transpose(-1, -2).contiguous().transpose(-1, -2).to(dtype)
+    assert np.array_equal(route_block_vote(view.to(DEV), 3, 16).cpu().numpy(), ref)
+
+
 def test_vote_config5_shape():
     # config 5: 32 heads, N = 16384, route block 128, p = 4, 4 levels, r = 2
     g = torch.Generator().manual_seed(5)
