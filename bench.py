@@ -14,8 +14,9 @@ the same step in one launch (routed_block_attention with the branch arity:
 the build runs inside the prefill kernel),
 sparse paged decode on config 4 (GB/s of routed KV bytes), the backward on
 config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), the
-ternary packed-K/V prefill over config 2's lists, one config-5 surgery layer
-(vote + build + prefill at N = 16384, GQA), and CPU baselines on the host
+ternary packed-K/V prefill over config 2's lists, config 5 end to end (a
+32-layer Llama-3.1-8B-shaped decoder, 16384-token prefill, whole forward and
+attention share, block-list attention at r = 2, 3, 4 against dense SDPA), and CPU baselines on the host
 cores: the fp32 masked-dense reference (oracle) on a bounded sample of config
 2's heads, and the float64 decode oracle on the first sequences of config 4.
 Untimed steps run back to back for --spinup-ms before the warmup steps, so
@@ -69,7 +70,7 @@ def parse_args():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward measurement")
     ap.add_argument("--no-ternary", action="store_true", help="skip the ternary packed-K/V measurement")
-    ap.add_argument("--no-c5", action="store_true", help="skip the config-5 surgery-layer measurement")
+    ap.add_argument("--no-c5", action="store_true", help="skip the config-5 32-layer model measurement")
     ap.add_argument("--cpu-heads", type=int, default=32, help="heads timed for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU work for the CPU baseline (whole passes over --cpu-heads)")
@@ -177,6 +178,74 @@ def density_sweep(torch, wl, nat, dev, reps):
         torch.cuda.empty_cache()
     return out
 
+
+
+def surgery_model_c5(torch, dev, args):
+    """Config 5 end to end, as the reference times it (experiments/bench_surgery_prefill.py:
+    81-108, 146-178): a 32-layer Llama-3.1-8B-shaped decoder (random-init bf16 weights, seeded
+    N(0, 1) tree-routing scores per layer, p 4, 4 levels) runs a 16384-token prefill of seeded
+    random token ids, without the LM head. Conditions: dense_sdpa (the unmodified model: torch's
+    SDPA, causal, key / value heads repeated) and block_list@r for r in {2, 3, 4} (route-block
+    vote, sync-free lists, GQA block-sparse prefill); block_list@0 lists every causal block, the
+    dense model on this build's kernel. Each condition: one untimed pass that
+    collects the list statistics, `warm` untimed passes, then `reps` timed passes; medians of
+    the whole forward (HIP events) and of the summed attention-block time (events around each
+    layer's projections + RoPE + routing + attention + output projection, the reference's
+    attention-module hooks)."""
+    from ultrametric.llama_model import LLAMA31_8B, SurgeryLlama
+    warm, reps, S = 2, 5, 16384
+    log("config 5: building the 32-layer model")
+    model = SurgeryLlama(LLAMA31_8B, device=dev, seed=0)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    ids = torch.randint(0, LLAMA31_8B.vocab, (1, S), generator=g).to(dev)
+    med = lambda xs: sorted(xs)[len(xs) // 2]  # noqa: E731
+    conds = []
+    for name, attn, r in (("dense_sdpa", "sdpa", 0), ("block_list@0", "block_list", 0),
+                          ("block_list@2", "block_list", 2), ("block_list@3", "block_list", 3),
+                          ("block_list@4", "block_list", 4)):
+        model.attention, model.r = attn, r
+        rec = {"condition": name}
+        with torch.no_grad():
+            if attn == "block_list":
+                model(ids, collect_stats=True)
+                st = model.last_stats
+                rec["block_density"] = round(sum(x["block_density"] for x in st) / len(st), 5)
+                rec["measured_budget"] = round(sum(x["mean_allowed_keys"] for x in st) /
+                                               sum(x["mean_causal_keys"] for x in st), 5)
+            for _ in range(warm):
+                model(ids)
+            torch.cuda.synchronize()
+            torch.cuda.reset_peak_memory_stats(dev)
+            totals, attns = [], []
+            for _ in range(reps):
+                model.attn_events = []
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                model(ids)
+                e.record()
+                torch.cuda.synchronize()
+                totals.append(s.elapsed_time(e))
+                attns.append(sum(a.elapsed_time(b) for a, b in model.attn_events))
+                model.attn_events = None
+        rec.update({"total_ms": round(med(totals), 2), "total_ms_all": [round(x, 2) for x in totals],
+                    "attn_ms": round(med(attns), 2),
+                    "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 1024 ** 3, 2)})
+        log(f"config 5 {name}: forward {rec['total_ms']:.1f} ms, attention {rec['attn_ms']:.1f} ms")
+        conds.append(rec)
+    dense = conds[0]
+    for rec in conds[1:]:
+        rec["speedup_total_vs_dense"] = round(dense["total_ms"] / rec["total_ms"], 3)
+        rec["speedup_attn_vs_dense"] = round(dense["attn_ms"] / rec["attn_ms"], 3)
+    del model, ids
+    return {
+        "workload": "config5: Llama-3.1-8B-shaped decoder, 32 layers, d 4096, 32 q / 8 kv heads, D 128, SwiGLU "
+                    "14336, RoPE theta 5e5, random-init bf16 weights; per-layer seeded N(0,1) routing scores "
+                    "(p 4, 4 levels), route block 128, local window 16 (1 block), sink; 16384-token prefill of "
+                    "seeded random ids, no LM head",
+        "timing": f"median of {reps} forwards after {warm} warmup + 1 statistics pass; attn_ms = summed HIP-event "
+                  "time of the 32 attention blocks (q/k/v projections, RoPE, routing, attention, o projection)",
+        "conditions": conds,
+    }
 
 def main():
     args = parse_args()
@@ -397,38 +466,10 @@ def main():
         log(f"ternary prefill {tern_ms * 1e3:.1f} us, {flop_alg / (tern_ms * 1e-3) / 1e12:.0f} TFLOP/s")
         del qh, kp, vp, ksc, vsc, tout
 
-    # ---------------- config 5: one surgery layer (vote + sync-free build + prefill) -----
+    # ---------------- config 5: 32-layer Llama-shaped prefill, block-list vs dense SDPA ---
     if not args.no_c5:
-        from ultrametric import block_list_prefill
-        g5 = torch.Generator(device="cpu").manual_seed(5)
-        S5, H5, Hkv5, L5, p5, r5 = 16384, 32, 8, 4, 4, 2
-        q5 = torch.randn(1, H5, S5, D, generator=g5).to(torch.bfloat16).to(dev)
-        k5 = torch.randn(1, Hkv5, S5, D, generator=g5).to(torch.bfloat16).to(dev)
-        v5 = torch.randn(1, Hkv5, S5, D, generator=g5).to(torch.bfloat16).to(dev)
-        a5 = torch.randn(1, H5, S5, L5, p5, generator=g5).to(dev)
-
-        def layer():
-            return block_list_prefill(q5, k5, v5, a5, r5, p=p5, route_block=RB, local_window=16)
-
-        with torch.no_grad():
-            for _ in range(3):
-                layer()
-            c5_ms = time_launches(layer, 20, torch)
-            _, st5 = block_list_prefill(q5, k5, v5, a5, r5, p=p5, route_block=RB, local_window=16,
-                                        return_stats=True)
-        tiles5 = st5["block_density"] * H5 * (S5 // RB) * (S5 // RB + 1) / 2
-        flop5 = 4 * D * RB * RB * tiles5
-        result["surgery_layer_c5"] = {
-            "workload": "config5 layer: Llama-3.1-8B shape, N 16384, 32 q / 8 kv heads (GQA native), D 128, "
-                        "route block 128, p 4, 4 levels, r 2, sink + 1 local block; per-token scores voted "
-                        "per block, sync-free lists, prefill; bf16",
-            "ms_per_layer": round(c5_ms, 5),
-            "block_density_causal": round(st5["block_density"], 4),
-            "tflops_computed_tiles": round(flop5 / (c5_ms * 1e-3) / 1e12, 1),
-            "ms_32_layers": round(32 * c5_ms, 4),
-        }
-        log(f"surgery layer (config 5) {c5_ms * 1e3:.1f} us, density {st5['block_density']:.3f}")
-        del q5, k5, v5, a5
+        result["surgery_prefill_c5"] = surgery_model_c5(torch, dev, args)
+        torch.cuda.empty_cache()
 
     # ---------------- config 3: density sweep (optional) ------------------------------
     if args.sweep:

@@ -124,7 +124,11 @@ def block_list_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, assign
     if route_cache is not None and layer_idx is not None:
         bl = route_cache.lookup(int(layer_idx), key)
     if bl is None:
-        if block_assignments is not None and block_assignments.shape[2] == NB:
+        if int(r) == 0:
+            # no routed level: every block matches (the list build needs a
+            # routing vector of at least one level; depth 0 never reads it)
+            route = torch.zeros((B, H, NB, 1), dtype=torch.int32, device=q.device)
+        elif block_assignments is not None and block_assignments.shape[2] == NB:
             route = route_block_vote(block_assignments[:, :, :NB], r, 1)
         elif assignments.shape[2] == NB and NB != S:
             route = route_block_vote(assignments[:, :, :NB], r, 1)
