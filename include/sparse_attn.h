@@ -414,6 +414,52 @@ int sa_ternary_prefill_fwd(const void* q, const int32_t* k_packed, const int32_t
 int sa_route_block_vote(const void* assign, int dtype, const int64_t* strides, int B, int H, int S,
                         int L, int p, int r, int route_block, int32_t* out, void* stream);
 
+/*
+ * Writes new tokens into a paged KV cache and their pages' routing codes into
+ * the per-sequence code array of sa_sparse_paged_decode_seq_codes.
+ * Replaces the reference's decode-time cache update (the transformers cache
+ * concatenating each layer's new K / V, which the eager decode masks of
+ * src/llama_surgery/surgery.py:880-955 then scan token by token); the paged
+ * layout is that of ultrametric_decode (src/ultrametric/kernel_decode.py:
+ * 188-247), which has no writer in the reference.
+ *
+ * k_new, v_new (B, H_kv, T, D), dtype, strides kn_strides[4] / vn_strides[4]
+ *             (the head dimension contiguous).
+ * n_new       (B,) int32 tokens of each sequence (<= T), or NULL: T each.
+ * context_lens (B,) int32: lengths that ALREADY include the new tokens
+ *             (sa_paged_advance first): token t of sequence b lands at
+ *             position context_lens[b] - n_new[b] + t, i.e. page slot
+ *             pos / page_size (physical page block_tables[b, slot]), row
+ *             pos % page_size.
+ * k_cache, v_cache (P = num_pages, H_kv, page_size, D), strides kc / vc[4].
+ * block_tables (B, max_pages) int32, strides bt_strides[2]; the pages must be
+ *             allocated by the caller beforehand.
+ * token_codes (B, H, T) uint32 packed routing codes of the new tokens
+ *             (sa_pack_page_codes layout), strides tc_strides[3], and
+ *             seq_codes (B, H, max_pages) of code_bytes (1, 2, 4) bytes,
+ *             strides sc_strides[3]: a page's code is the code of its first
+ *             token (position % page_size == 0), the first-token rule of
+ *             routing_to_block_indices (src/ultrametric/kernel.py:152-191).
+ *             Either NULL: no codes are written.
+ * status      NULL or one int32: bit 0 is set (atomic OR) for a token whose
+ *             page slot is >= max_pages or whose physical page is outside
+ *             [0, num_pages); such tokens are not written.
+ */
+int sa_paged_kv_write(const void* k_new, const void* v_new, const int64_t* kn_strides,
+                      const int64_t* vn_strides, const uint32_t* token_codes, const int64_t* tc_strides,
+                      const int32_t* n_new, int B, int H_kv, int T, int D, int H, void* k_cache,
+                      void* v_cache, const int64_t* kc_strides, const int64_t* vc_strides,
+                      const int32_t* block_tables, const int64_t* bt_strides, const int32_t* context_lens,
+                      int max_pages, int num_pages, int page_size, void* seq_codes, int code_bytes,
+                      const int64_t* sc_strides, int dtype, int32_t* status, void* stream);
+
+/*
+ * context_lens[b] += n_new[b] (n_new NULL: += T) for b < B, on the device.
+ * Companion of sa_paged_kv_write (same reference counterpart): one launch per
+ * model step, before the layers write their K / V.
+ */
+int sa_paged_advance(int32_t* context_lens, const int32_t* n_new, int B, int T, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

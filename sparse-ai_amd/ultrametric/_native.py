@@ -61,6 +61,9 @@ _SIGNATURES = {
     "sa_block_sparse_bwd_plan_bytes": (ctypes.c_size_t, [_I, _I, _I, _I, _I, _I]),
     "sa_block_sparse_bwd_plan": (_I, [_P, _P, _I, _P, _P, _I, _P, _I, _I64P, _I, _I, _I, _I, _I, _P,
                                       ctypes.c_size_t, _P, _P]),
+    "sa_paged_kv_write": (_I, [_P, _P, _I64P, _I64P, _P, _I64P, _P, _I, _I, _I, _I, _I, _P, _P, _I64P, _I64P,
+                               _P, _I64P, _P, _I, _I, _I, _P, _I, _I64P, _I, _P, _P]),
+    "sa_paged_advance": (_I, [_P, _P, _I, _I, _P]),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 

@@ -28,6 +28,7 @@ from typing import List, Optional
 import torch
 import torch.nn.functional as F
 
+from .paged_cache import PagedKVCache, token_routing_codes
 from .surgery import RouteCache, block_list_prefill
 
 __all__ = ["LlamaShape", "LLAMA31_8B", "SurgeryLlama", "rope_tables", "apply_rope"]
@@ -113,6 +114,8 @@ class SurgeryLlama:
         self.attention = "block_list"
         self.attn_events: Optional[list] = None   # (start, end) CUDA events per layer when set to a list
         self.last_stats: Optional[list] = None
+        self._fill: Optional[PagedKVCache] = None  # cache that a forward writes its K / V into
+        self.bits_per_level = max(1, (self.p - 1).bit_length())
 
     # -- routing scores ---------------------------------------------------------------
     def routing_scores(self, layer: int, batch: int, seq_len: int) -> torch.Tensor:
@@ -173,6 +176,9 @@ class SurgeryLlama:
         """Projections, RoPE, routing, attention and output projection of one layer."""
         B, S, _ = x.shape
         q, k, v = self.qkv(layer, x)
+        if self._fill is not None:
+            levels = self.routing_scores(layer, B, S)[..., :self.levels, :].argmax(-1)   # (B, H, S, levels)
+            self._fill.write(layer, k, v, token_routing_codes(levels, self.bits_per_level))
         o = self.core_attention(layer, q, k, v, collect_stats)
         o = o.transpose(1, 2).reshape(B, S, self.shape.heads * self.shape.head_dim)
         return F.linear(o, self.layers[layer]["wo"])
@@ -205,3 +211,74 @@ class SurgeryLlama:
             x = x + a
             x = x + self.mlp(li, _rms_norm(x, L["ln2"], sh.rms_eps))
         return _rms_norm(x, self.norm, sh.rms_eps)
+
+    # -- serving: paged prefill and single-token decode -----------------------------------
+    def new_cache(self, max_seqs: int, max_tokens: int, page_size: int = 16, num_pages: Optional[int] = None,
+                  layers: Optional[int] = None) -> PagedKVCache:
+        """A paged cache for ``layers`` layers (all by default), room for ``max_tokens`` per sequence."""
+        sh = self.shape
+        max_pages = -(-max_tokens // page_size)
+        return PagedKVCache(num_pages or max_seqs * max_pages, page_size, sh.kv_heads, sh.head_dim, heads=sh.heads,
+                            tree_depth=self.levels, bits_per_level=self.bits_per_level, max_seqs=max_seqs,
+                            max_pages_per_seq=max_pages, layers=sh.layers if layers is None else layers,
+                            dtype=self.dtype, device=self.device)
+
+    @torch.no_grad()
+    def prefill(self, cache: PagedKVCache, input_ids: torch.Tensor, *, layers: Optional[int] = None) -> torch.Tensor:
+        """Prompt forward (the block-list or SDPA condition) that also stores every layer's
+        K / V and page codes (first token of each page, from that layer's routing
+        scores) in rows 0 .. B-1 of ``cache``, which must be empty there."""
+        B, S = input_ids.shape
+        if any(cache.lengths[b] for b in range(B)):
+            raise ValueError("prefill needs empty cache rows")
+        cache.reserve(S, rows=range(B))
+        cache.advance(S, B)
+        self._fill = cache
+        try:
+            return self(input_ids, layers=layers)
+        finally:
+            self._fill = None
+
+    def decode_levels(self, scores: torch.Tensor) -> torch.Tensor:
+        """(B, H, levels, p) routing scores of new tokens -> (B, H) int32 packed codes."""
+        lv = scores[..., :self.levels, :].argmax(-1).to(torch.int32)
+        return token_routing_codes(lv.unsqueeze(2), self.bits_per_level)[:, :, 0]
+
+    def local_pages(self, page_size: int) -> int:
+        """Trailing pages that cover the local window ending at the new token."""
+        return 0 if self.local_window <= 0 else -(-self.local_window // page_size) + 1
+
+    @torch.no_grad()
+    def decode_step(self, cache: PagedKVCache, input_ids: torch.Tensor, scores: torch.Tensor, *,
+                    layers: Optional[int] = None) -> torch.Tensor:
+        """One new token per row 0 .. B-1: input_ids (B,), scores (layers, B, H, levels, p)
+        routing scores of the new tokens. The reference's eager decode mask
+        (src/llama_surgery/surgery.py:880-955: the token's branch over r levels equal to
+        a past token's, a local window, token 0) becomes page selection over the paged
+        cache: a page whose first token's code matches the new token's on r levels,
+        page 0 (the sink) and the pages of the local window. Every launch reads its
+        sizes from the device (lengths, tables), so the step can be captured in a HIP
+        graph once ``cache.reserve`` has pages for it. Returns hidden states (B, hidden)."""
+        sh = self.shape
+        n = sh.layers if layers is None else int(layers)
+        B = input_ids.shape[0]
+        pos = cache.context_lens[:B].long()              # position of the new token
+        cache.advance(1, B)
+        cos, sin = self._rope_for(cache.max_pages * cache.page_size)
+        cos, sin = cos[pos][:, None, None, :], sin[pos][:, None, None, :]
+        x = F.embedding(input_ids, self.embed)[:, None, :]   # (B, 1, hidden)
+        hd = sh.head_dim
+        for li in range(n):
+            L = self.layers[li]
+            h = _rms_norm(x, L["ln1"], sh.rms_eps)
+            q = F.linear(h, L["wq"]).view(B, sh.heads, 1, hd)
+            k = F.linear(h, L["wk"]).view(B, sh.kv_heads, 1, hd)
+            v = F.linear(h, L["wv"]).view(B, sh.kv_heads, 1, hd)
+            q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+            codes = self.decode_levels(scores[li])
+            cache.write(li, k, v, codes.unsqueeze(-1))
+            o = cache.decode(li, q[:, :, 0], codes, self.r, local_blocks=self.local_pages(cache.page_size),
+                             sink_block=True)
+            x = x + F.linear(o.reshape(B, 1, sh.heads * hd), L["wo"])
+            x = x + self.mlp(li, _rms_norm(x, L["ln2"], sh.rms_eps))
+        return _rms_norm(x, self.norm, sh.rms_eps)[:, 0]
