@@ -19,7 +19,10 @@
  *     sa_last_error() then returns a thread-local message. Argument errors are
  *     detected on the host before any launch.
  *   - Calls are reentrant; the library keeps no global mutable state apart
- *     from the thread-local error string.
+ *     from the thread-local error string and, for
+ *     sa_sparse_paged_decode_seq_codes_noalloc only, one 8 MiB device array
+ *     per GPU (the split-KV partials of that entry point) with its per-device
+ *     address.
  */
 #ifndef SPARSE_ATTN_H
 #define SPARSE_ATTN_H
@@ -459,6 +462,39 @@ int sa_paged_kv_write(const void* k_new, const void* v_new, const int64_t* kn_st
  * model step, before the layers write their K / V.
  */
 int sa_paged_advance(int32_t* context_lens, const int32_t* n_new, int B, int T, void* stream);
+
+/*
+ * sa_sparse_paged_decode_seq_codes without the workspace argument: the
+ * split-KV partials live in a file-scope device array of the library
+ * (sa_noalloc_scratch_bytes() bytes = 8 MiB per GPU, held until the process
+ * ends), so the call allocates nothing. 8 MiB holds the partials of every
+ * head_dim <= 128 problem (at most (512 + B H_kv) x G x (D + 2) floats).
+ * No counterpart in the reference. It is for callers that cannot allocate:
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.
+ * Same arguments (minus workspace / workspace_bytes) and same results as
+ * sa_sparse_paged_decode_seq_codes. The current HIP device must be the one
+ * the tensors and stream belong to; its array's address is looked up on the
+ * first call there. Returns SA_EINVAL when the partials need more than
+ * sa_noalloc_scratch_bytes() (sa_decode_workspace_bytes > 8 MiB). Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (concurrent streams) race; calls in one stream order are safe. Every
+ * partial the merge reads is written by the same call, so nothing needs
+ * clearing between calls.
+ */
+int sa_sparse_paged_decode_seq_codes_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                             const int32_t* block_tables, const int32_t* context_lens,
+                                             const void* seq_codes, int code_bytes, const uint32_t* q_codes,
+                                             void* out, int B, int H, int H_kv, int D, int page_size, int TD,
+                                             int bits_per_level, int max_pages, int num_phys_pages,
+                                             int req_depth, int local_blocks, int sink_block,
+                                             const int64_t* q_strides, const int64_t* k_strides,
+                                             const int64_t* v_strides, const int64_t* bt_strides,
+                                             const int64_t* sc_strides, const int64_t* qc_strides,
+                                             const int64_t* o_strides, int dtype, void* stream);
+
+/* Bytes of the no-allocation entry point's per-GPU scratch array. */
+size_t sa_noalloc_scratch_bytes(void);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,7 @@
 // combines. Consecutive work items (the kv heads of one sequence, which read
 // the same block-table and router rows) are placed on one XCD.
 #include "sa_internal.h"
+#include <mutex>
 
 namespace sa {
 namespace {
@@ -914,4 +915,70 @@ extern "C" int sa_pack_page_codes(const int32_t* router, const int64_t* strides,
   hipLaunchKernelGGL(pack_codes_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, as_stream(stream), router,
                      strides[0], strides[1], strides[2], rows, H, TD, bits_per_level, codes);
   return check_launch("page-code packing kernel");
+}
+
+// ---- no-allocation decode: split-KV partials in a file-scope device array ------
+// One array per GPU, held until the process ends. Host code never passes the
+// array's name to a kernel (in host code it is a stand-in, not a device
+// address): the address each device gives for it is looked up once, with that
+// device current, and kept per device.
+namespace sa {
+namespace {
+constexpr size_t kNoAllocScratchBytes = static_cast<size_t>(8) << 20;   // every D <= 128 case fits
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+}  // namespace sa
+
+static __device__ __align__(256) unsigned char scratch[sa::kNoAllocScratchBytes];
+
+namespace sa {
+namespace {
+// Device address of `scratch` on the current device (looked up on the first call there).
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(SA_ELAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(SA_EUNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      return fail(SA_ELAUNCH, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return SA_OK;
+}
+}  // namespace
+}  // namespace sa
+
+extern "C" size_t sa_noalloc_scratch_bytes(void) { return sa::kNoAllocScratchBytes; }
+
+extern "C" int sa_sparse_paged_decode_seq_codes_noalloc(
+    const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+    const int32_t* context_lens, const void* seq_codes, int code_bytes, const uint32_t* q_codes, void* out, int B,
+    int H, int H_kv, int D, int page_size, int TD, int bits_per_level, int max_pages, int num_phys_pages,
+    int req_depth, int local_blocks, int sink_block, const int64_t* q_strides, const int64_t* k_strides,
+    const int64_t* v_strides, const int64_t* bt_strides, const int64_t* sc_strides, const int64_t* qc_strides,
+    const int64_t* o_strides, int dtype, void* stream) {
+  using namespace sa;
+  const size_t need = sa_decode_workspace_bytes(B, H, H_kv, D, max_pages);
+  if (need > kNoAllocScratchBytes) {
+    return fail(SA_EINVAL, "split-KV partials need " + std::to_string(need) + " bytes, more than the " +
+                               std::to_string(kNoAllocScratchBytes) + " of the no-allocation scratch");
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_on_current_device(&ws);
+    if (rc != SA_OK) return rc;
+  }
+  return sa_sparse_paged_decode_seq_codes(q, k_cache, v_cache, block_tables, context_lens, seq_codes, code_bytes,
+                                          q_codes, out, B, H, H_kv, D, page_size, TD, bits_per_level, max_pages,
+                                          num_phys_pages, req_depth, local_blocks, sink_block, q_strides,
+                                          k_strides, v_strides, bt_strides, sc_strides, qc_strides, o_strides, ws,
+                                          need > 0 ? kNoAllocScratchBytes : 0, dtype, stream);
 }

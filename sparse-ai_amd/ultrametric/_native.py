@@ -64,6 +64,10 @@ _SIGNATURES = {
     "sa_paged_kv_write": (_I, [_P, _P, _I64P, _I64P, _P, _I64P, _P, _I, _I, _I, _I, _I, _P, _P, _I64P, _I64P,
                                _P, _I64P, _P, _I, _I, _I, _P, _I, _I64P, _I, _P, _P]),
     "sa_paged_advance": (_I, [_P, _P, _I, _I, _P]),
+    "sa_sparse_paged_decode_seq_codes_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                                      _I, _I, _I, _I, _I, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
+                                                      _I64P, _I, _P]),
+    "sa_noalloc_scratch_bytes": (ctypes.c_size_t, []),
 }
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
