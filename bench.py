@@ -17,13 +17,18 @@ config 2 (dQ, dK, dV; algorithmic TFLOP/s = 2.5 x the forward's), the
 ternary packed-K/V prefill over config 2's lists, config 5 end to end (a
 32-layer Llama-3.1-8B-shaped decoder, 16384-token prefill, whole forward and
 attention share, block-list attention at r = 2, 3, 4 against dense SDPA), and CPU baselines on the host
-cores: the fp32 masked-dense reference (oracle) on a bounded sample of config
-2's heads, and the float64 decode oracle on the first sequences of config 4.
+cores (below).
 Untimed steps run back to back for --spinup-ms before the warmup steps, so
-that the timed steps run at the GPU's steady clocks.
+that the timed steps run at the GPU's steady clocks. The config-3 density
+sweep runs by default (--no-sweep skips it). CPU baselines (--no-cpu skips
+them, --cpu-quick keeps only config 2's): the fp32 masked-dense reference on
+the host cores for configs 1, 2, 3 (N <= 8192 all heads; N = 32768 one head
+x 32) and one config-5 layer (two heads x 16), and the float64 decode oracle
+over all 64 x 32 (sequence, head) pairs of config 4; each a median of 3 runs
+after a warm-up, recorded with the CPU model, cores and torch threads.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup-ms MS] [--no-cpu] [--no-decode]
-                       [--no-backward] [--no-ternary] [--no-c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--spinup-ms MS] [--no-cpu] [--cpu-quick]
+                       [--no-decode] [--no-backward] [--no-ternary] [--no-c5] [--no-sweep]
 Only one GPU is supported: --gpus N > 1 exits with a message.
 """
 
@@ -66,7 +71,9 @@ def parse_args():
     ap.add_argument("--spinup-ms", type=float, default=200.0,
                     help="untimed steps run back to back for this long before the warmup steps, so that "
                          "the timed steps run at the GPU's steady clocks")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-quick", action="store_true",
+                    help="CPU baseline of config 2 only (the headline), not the per-config records")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode measurement")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward measurement")
     ap.add_argument("--no-ternary", action="store_true", help="skip the ternary packed-K/V measurement")
@@ -74,22 +81,109 @@ def parse_args():
     ap.add_argument("--cpu-heads", type=int, default=32, help="heads timed for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU work for the CPU baseline (whole passes over --cpu-heads)")
-    ap.add_argument("--sweep", action="store_true",
-                    help="also run config 3: density sweep at N in {2048, 8192, 32768} against the dense case")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip config 3: the density sweep at N in {2048, 8192, 32768} against the dense case")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (reference for HBM byte counters)")
     return ap.parse_args()
 
 
 def cpu_model():
+    """CPU model string plus family / model / stepping and socket count from /proc/cpuinfo."""
+    fields, sockets = {}, set()
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    continue
+                key, val = (x.strip() for x in line.split(":", 1))
+                if key == "physical id":
+                    sockets.add(val)
+                elif key in ("model name", "cpu family", "model", "stepping", "vendor_id") and key not in fields:
+                    fields[key] = val
     except OSError:
         pass
-    return platform.processor() or platform.machine()
+    name = fields.get("model name") or platform.processor() or platform.machine()
+    extra = ", ".join(f"{k} {fields[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({extra}; {max(1, len(sockets))} socket(s))" if extra else name
+
+
+def cpu_info(torch):
+    return {"cpu_model": cpu_model(), "cpu_cores": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "torch": torch.__version__}
+
+
+def median_wall(fn, runs=3):
+    """One warm-up call, then the median wall time (s) of `runs` calls (BASELINE: >= 3 runs)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baselines(torch, wl, dev):
+    """Per-configuration CPU baselines (BASELINE.md: masked-dense fp32 reference on the host cores;
+    configs 1 and 3 at N <= 8192 on all heads, config 3 at N = 32768 on one head scaled by 32,
+    config 5 on two of the 32 heads of one layer scaled by 16). Each record: wall time (median of
+    3 runs after a warm-up), FLOP_alg of the timed work and the equivalent TFLOP/s."""
+    from oracle import attention as oa
+    from ultrametric import block_lists_from_mask
+    out = {}
+    # config 1: fp32, all 4 heads
+    c1 = wl.config1()
+    bm1 = c1["block_mask"][0]
+    bl1 = block_lists_from_mask(c1["block_mask"].to(dev), is_causal=True)
+    f1 = wl.prefill_flops(bl1.counts, 64, 64)
+    w1 = median_wall(lambda: oa.masked_attention_torch_fp32(c1["q"][0], c1["k"][0], c1["v"][0], bm1, 64, True))
+    out["config1"] = {"shape": "fp32 Z1 H4 N1024 D64 RB64 causal, Bernoulli(0.25) + diag + sink", "seed": 1,
+                      "heads_timed": 4, "wall_ms": round(w1 * 1e3, 3), "flop_alg": f1,
+                      "tflops": round(f1 / w1 / 1e12, 5)}
+    log(f"cpu config1 {w1 * 1e3:.1f} ms")
+    # config 3: one timing per N (the masked-dense work does not depend on the density),
+    # FLOP_alg per density of that N's listed tiles
+    for N in (2048, 8192, 32768):
+        NB = N // 128
+        heads = 32 if N <= 8192 else 1
+        g = torch.Generator().manual_seed(3)
+        q, k, v = (torch.randn(1, heads, N, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+        bm = wl.bernoulli_block_mask(1, heads, NB, 0.25, seed=3 + int(0.25 * 1e6))[0]
+        w = median_wall(lambda: oa.masked_attention_torch_fp32(q[0], k[0], v[0], bm, 128, True))
+        per = {}
+        for rho in (1.0, 0.5, 0.25, 0.0625, 0.016):
+            m = wl.bernoulli_block_mask(1, 32, NB, rho, seed=3 + int(rho * 1e6))
+            cnt = m.sum(-1).to(torch.int32)
+            f = wl.prefill_flops(cnt[:, :heads], 128, 128)
+            per[str(rho)] = {"flop_alg": f * (32 // heads), "tflops": round(f / w / 1e12, 5)}
+        out[f"config3_N{N}"] = {
+            "shape": f"bf16 Z1 H32 N{N} D128 RB128 causal, fp32 masked-dense on the host", "seed": 3,
+            "heads_timed": heads, "scaled_to_32_heads": heads != 32,
+            "wall_ms": round(w * 1e3 * (32 // heads), 3), "wall_ms_timed": round(w * 1e3, 3), "per_density": per}
+        log(f"cpu config3 N={N} {w * 1e3:.1f} ms on {heads} head(s)")
+        del q, k, v
+    # config 5: one layer's attention at N = 16384 (32 q / 8 kv heads), two query heads timed
+    g = torch.Generator().manual_seed(5)
+    S5, heads5 = 16384, 2
+    q5 = torch.randn(heads5, S5, 128, generator=g).to(torch.bfloat16)
+    k5 = torch.randn(1, S5, 128, generator=g).to(torch.bfloat16)
+    v5 = torch.randn(1, S5, 128, generator=g).to(torch.bfloat16)
+    a5 = torch.randn(1, 32, S5, 4, 4, generator=g)
+    from oracle import blocks as ob
+    from oracle import surgery as osg
+    route = osg.majority_route(a5.numpy(), 2, 128)
+    bl5 = ob.build_block_lists(route, 2, is_causal=True, sink_block=True, local_blocks=1, arity=4)
+    bm5 = torch.from_numpy(ob.lists_to_mask(bl5.lists, bl5.counts))[0, :heads5]
+    w5 = median_wall(lambda: oa.masked_attention_torch_fp32(q5, k5, v5, bm5, 128, True))
+    f5 = wl.prefill_flops(torch.from_numpy(bl5.counts)[0, :heads5], 128, 128)
+    out["config5_layer"] = {
+        "shape": "one Llama-3.1-8B attention layer: bf16 N16384 32 q / 8 kv heads D128 RB128, r 2 of 4 levels, "
+                 "p 4, sink + 1 local block; fp32 masked-dense on the host", "seed": 5,
+        "heads_timed": heads5, "scaled_to_32_heads": True, "wall_ms": round(w5 * 1e3 * 16, 3),
+        "wall_ms_timed": round(w5 * 1e3, 3), "flop_alg": f5 * 16, "tflops": round(f5 / w5 / 1e12, 5)}
+    log(f"cpu config5 layer {w5 * 1e3:.1f} ms on {heads5} heads")
+    return out
 
 
 def log(msg):
@@ -383,6 +477,7 @@ def main():
             "active_tiles": n_tiles, "tile_density_full": round(n_tiles / total_tiles, 5),
             "tile_density_causal": round(n_tiles / causal_tiles, 5),
             "flop_alg": flop_alg, "flop_useful_token_exact": useful,
+            "useful_fraction_of_computed": round(useful / flop_alg, 4),
             "parallelism": "single GPU",
         },
         "prefill_kernel_ms": round(fwd_ms, 5),
@@ -471,8 +566,8 @@ def main():
         result["surgery_prefill_c5"] = surgery_model_c5(torch, dev, args)
         torch.cuda.empty_cache()
 
-    # ---------------- config 3: density sweep (optional) ------------------------------
-    if args.sweep:
+    # ---------------- config 3: density sweep ------------------------------------------
+    if not args.no_sweep:
         result["sweep"] = density_sweep(torch, wl, nat, dev, reps=max(20, args.steps // 4))
 
     # ---------------- config 4: sparse paged decode -----------------------------------
@@ -578,46 +673,67 @@ def main():
             "frac": round(sgbs / PEAK_HBM_GBS, 4),
             "layout": f"(B, H, max_pages) {8 * sc.element_size()}-bit codes in logical page order, read with the block table",
         }
+        # the roofline is quoted on the serving layout (sequence codes); the reference
+        # layout (int32 levels per physical page and head) scans ~36 MB of scattered
+        # router lines on top of the routed bytes, so it sits beside it
+        result["decode"]["roofline_reference_layout"] = result["decode"]["roofline"]
+        result["decode"]["roofline"] = {
+            "kernel": "decode_kernel<bf16, D=128, G=4, mode 2 (sequence codes)>", "bound": "hbm",
+            "achieved": round(sgbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(sgbs / PEAK_HBM_GBS, 4),
+            "traffic": profiled_traffic("decode_config4_seqcodes_bf16.md"),
+            "traffic_source": "profiles/decode_config4_seqcodes_bf16.md"}
         log(f"decode (sequence codes) {sdec_ms * 1e3:.1f} us/call, {sgbs:.0f} GB/s on routed bytes")
 
         if not args.no_cpu:
             # decode: the float64 loop oracle (the reference's _ultrametric_decode_reference
-            # semantics, GQA grouped) over the first sequences of config 4, with only their
-            # pages copied to the host
+            # semantics, GQA grouped) over all 64 sequences x 32 heads of config 4 (with
+            # --cpu-quick the first 4 sequences). Only the pages some head of a sequence selects
+            # are copied to the host; every other table slot points at a page whose routing
+            # vector matches no query, so the oracle selects exactly what it would on the full
+            # cache.
             import numpy as np
             from oracle import decode as od
-            ns = min(4, B)
-            ctx_s = w.context_lens[:ns].cpu().numpy().astype(np.int64)
-            npg = (ctx_s + PS - 1) // PS
-            bt_s = w.block_tables[:ns].cpu().numpy().astype(np.int64)
-            used = np.unique(np.concatenate([bt_s[i, :npg[i]] for i in range(ns)]))
-            bt_c = np.zeros_like(bt_s)
-            for i in range(ns):
-                bt_c[i, :npg[i]] = np.searchsorted(used, bt_s[i, :npg[i]])
-            used_t = torch.from_numpy(used).to(dev)
-            kc_s = w.k_cache[used_t].float().cpu().numpy()
-            vc_s = w.v_cache[used_t].float().cpu().numpy()
-            r_s = w.router[used_t].cpu().numpy()
+            ns = 4 if args.cpu_quick else B
+            r_d = min(max(int(w.req_depth), 0), TD)
+            ctx_t = w.context_lens[:ns].long()
+            npg_t = (ctx_t + PS - 1) // PS
+            lpos = torch.arange(max_pages, device=dev)[None, :]
+            valid = lpos < npg_t[:, None]
+            phys = w.block_tables[:ns].long().clamp(0, P - 1)
+            sel = (w.router[phys][..., :r_d] == w.q_router[:ns, None, :, :r_d]).all(-1).any(-1)
+            if w.sink_block:
+                sel |= lpos == 0
+            if w.local_blocks > 0:
+                sel |= lpos >= (npg_t[:, None] - w.local_blocks)
+            sel &= valid
+            used = torch.unique(phys[sel])
+            remap = torch.zeros(P, dtype=torch.long, device=dev)
+            remap[used] = torch.arange(1, used.numel() + 1, device=dev)
+            bt_c = torch.where(sel, remap[phys], torch.zeros_like(phys)).cpu().numpy()
+            ctx_s = ctx_t.cpu().numpy()
+
+            def compact(t):
+                body = t[used].float()
+                return torch.cat([torch.zeros_like(body[:1]), body]).cpu().numpy()
+
+            kc_s, vc_s = compact(w.k_cache), compact(w.v_cache)
+            r_s = w.router[used].cpu().numpy()
+            r_s = np.concatenate([np.full((1,) + r_s.shape[1:], -1, dtype=r_s.dtype), r_s])
             q_s = w.q[:ns].float().cpu().numpy()
             qr_s = w.q_router[:ns].cpu().numpy()
-            od.decode_reference(q_s[:1], kc_s, vc_s, bt_c[:1], ctx_s[:1], r_s, qr_s[:1], **kw)
-            dpasses, t0 = 0, time.perf_counter()
-            while True:
-                od.decode_reference(q_s, kc_s, vc_s, bt_c, ctx_s, r_s, qr_s, **kw)
-                dpasses += 1
-                if time.perf_counter() - t0 >= min(args.cpu_seconds, 5.0):
-                    break
-            dcpu_s = (time.perf_counter() - t0) / dpasses
+            dcpu_s = median_wall(lambda: od.decode_reference(q_s, kc_s, vc_s, bt_c, ctx_s, r_s, qr_s, **kw))
             b_s, _ = od.routed_page_bytes(bt_c, ctx_s, r_s, qr_s, Hkv, PS, Dd, 2, **kw)
             result["decode"]["cpu_baseline"] = {
                 "value": round(b_s / dcpu_s / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
                 "kind": "port",
                 "sample": f"float64 decode oracle (oracle/decode.py decode_reference, the reference's "
-                          f"_ultrametric_decode_reference loop) on the first {ns} of {B} sequences, all "
-                          f"{Hq} heads; {dpasses} passes, {dcpu_s * 1e3:.1f} ms per pass; value = routed "
-                          f"bytes of those sequences / wall time per pass",
+                          f"_ultrametric_decode_reference loop) on {ns} of {B} sequences x all {Hq} heads, "
+                          f"median of 3 passes after a warm-up: {dcpu_s * 1e3:.1f} ms per pass; value = "
+                          f"routed bytes of those sequences / wall time per pass",
+                "wall_ms": round(dcpu_s * 1e3, 3), "bytes_alg": int(b_s), "sequences": ns, "seed": 4,
             }
             log(f"decode cpu baseline {dcpu_s * 1e3:.1f} ms per pass over {ns} sequences")
+            del kc_s, vc_s
         del w
 
     # ---------------- CPU baseline (oracle, host cores) --------------------------------
@@ -646,8 +762,19 @@ def main():
             "cpu_model": cpu_model(),
             "os_cpu_count": os.cpu_count(),
             "torch": torch.__version__,
+            "wall_ms": round(cpu_s * 1e3, 3), "flop_alg": flop_sample, "seed": 2,
         }
         log(f"cpu baseline {cpu_s:.2f} s per pass over {len(heads)} heads ({passes} passes)")
+        if not args.cpu_quick:
+            rec = {"info": cpu_info(torch)}
+            rec["config2"] = {"shape": "bf16 Z1 H32 N8192 D128 RB128 causal, tree routing p4 depth 3 LCA >= 2 "
+                                       "+ diag + sink; fp32 masked-dense on the host", "seed": 2,
+                              "heads_timed": len(heads), "wall_ms": round(cpu_s * 1e3, 3),
+                              "flop_alg": flop_sample, "tflops": result["cpu_baseline"]["value"]}
+            rec.update(cpu_baselines(torch, wl, dev))
+            if "decode" in result and "cpu_baseline" in result["decode"]:
+                rec["config4"] = dict(result["decode"]["cpu_baseline"])
+            result["cpu_baselines"] = rec
 
     print(json.dumps(result), flush=True)
 
