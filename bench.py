@@ -670,6 +670,8 @@ def main():
         sgbs = b_alg / (sdec_ms * 1e-3) / 1e9
         result["decode"]["sequence_codes"] = {
             "bits_per_level": bpl, "ms_per_call": round(sdec_ms, 5), "gbs_routed": round(sgbs, 1),
+            "routing_metadata_bytes": int(w.context_lens.add(15).div(16, rounding_mode="floor").sum())
+            * (4 + 32 * sc.element_size()),
             "frac": round(sgbs / PEAK_HBM_GBS, 4),
             "layout": f"(B, H, max_pages) {8 * sc.element_size()}-bit codes in logical page order, read with the block table",
         }
