@@ -35,7 +35,7 @@
 // otherwise it writes (m, l, acc[D]) partials that decode_merge_kernel
 // combines. Consecutive work items (the kv heads of one sequence, which read
 // the same block-table and router rows) are placed on one XCD.
-#include "sa_internal.h"
+#include "mfma_util.h"
 #include <mutex>
 
 namespace sa {
@@ -74,6 +74,7 @@ struct DecParams {
   int64_t qrs0, qrs1, qrs2;
   int64_t os0, os1, os2;
   float qk_scale;
+  int mfma_b;               // phase B on MFMA (see decode_kernel)
 };
 
 // DPL consecutive elements (unit stride) kept as raw 32-bit words.
@@ -149,9 +150,14 @@ __device__ __forceinline__ float row_dot(const uint32_t* a, const RowRegs<T, DPL
 // are contiguous, so thread t reads the codes and block-table entries of
 // pages 8t .. 8t+7 of a 2048-page range with wide loads issued in the
 // prologue, and builds their head masks in registers (no ballot).
-template <typename T, int D, int G, int MODE>
+// MB: phase B on MFMA (16-bit K / V, D in {32, 64, 128}, pages of at most 16
+// tokens, 16-byte aligned rows): per page S^T = K Q^T on 16x16x32 tiles (lane
+// = head of the group, 4 tokens per lane), O^T += V^T P^T on 16x16x16 tiles
+// with V^T read through this wave's LDS slot by transposing reads.
+template <typename T, int D, int G, int MODE, bool MB>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(G * D <= 512 ? 2 : 1)))
 void decode_kernel(DecParams p) {
+  static_assert(!MB || (sizeof(T) == 2 && (D == 32 || D == 64 || D == 128) && G <= 16), "MFMA phase B shapes");
   constexpr bool PACKED = MODE == 1;
   constexpr bool LOGICAL = MODE == 2;
   constexpr int DPL = D / 16;
@@ -177,6 +183,9 @@ void decode_kernel(DecParams p) {
   __shared__ float red_m[kDecWaves][G];
   __shared__ float red_l[kDecWaves][G];
   __shared__ float red_acc[kDecWaves][G][D];
+  // MFMA phase B: one page of V rows per wave (16 rows of 2D bytes), 32-byte
+  // units of row r stored at unit u ^ vunit(r).
+  __shared__ __attribute__((aligned(16))) char vstage[kDecWaves][MB ? 32 * D : 16];
 
   // Work items ordered (b, kv head, split); consecutive items (the kv heads of
   // one sequence, which read the same block-table row and router rows) share
@@ -293,12 +302,47 @@ void decode_kernel(DecParams p) {
   const bool qvec = p.qs2 == 1 && ((p.qs0 | p.qs1) * static_cast<int64_t>(sizeof(T))) % kQAlign == 0 &&
                     (reinterpret_cast<uintptr_t>(p.q) % kQAlign) == 0;
   float m_s[G], l_s[G], acc[G][DPL];
+  // MFMA phase B state: Q^T operand (lane l: head l % 16, elements
+  // 32 c + 8 (l / 16) .. +8), O^T tiles (lane l: head l % 16, d = 16 t + 4 (l / 16) + i),
+  // the running maximum of head l % 16 and this lane's part of its sum.
+  constexpr int KC = MB ? D / 32 : 1;
+  constexpr int DT16 = MB ? D / 16 : 1;
+  const int t16 = lane & 15, kg = lane >> 4;
+  u32x4_t qop[KC];
+  f32x4_t oacc[DT16];
+  float mb_m = -INFINITY, mb_l = 0.f;
+  if constexpr (MB) {
+#pragma unroll
+    for (int t = 0; t < DT16; ++t) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < KC; ++c) qop[c] = u32x4_t{0u, 0u, 0u, 0u};
+    if (t16 < G) {
+      const T* qp = static_cast<const T*>(p.q) + b * p.qs0 + (h0 + t16) * p.qs1;
+      const bool qv16 = p.qs2 == 1 && ((p.qs0 | p.qs1) * 2) % 16 == 0 && (reinterpret_cast<uintptr_t>(p.q) & 15) == 0;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int d0 = 32 * c + 8 * kg;
+        if (qv16) {
+          qop[c] = *reinterpret_cast<const u32x4_t*>(qp + d0);
+        } else {
+          uint32_t w[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            w[e] = elem_bits<T>(qp + (d0 + 2 * e) * p.qs2) | (elem_bits<T>(qp + (d0 + 2 * e + 1) * p.qs2) << 16);
+          }
+          qop[c] = u32x4_t{w[0], w[1], w[2], w[3]};
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const T* qp = static_cast<const T*>(p.q) + b * p.qs0 + (h0 + g) * p.qs1 + sub * DPL * p.qs2;
 #pragma unroll
     for (int i = 0; i < QW; ++i) qw[g][i] = 0u;
-    if (qvec) {
+    if (MB) {
+      // phase B reads qop
+    } else if (qvec) {
       RowRegs<T, DPL> qr;
       load_row<T, DPL>(qp, qr);
 #pragma unroll
@@ -540,7 +584,106 @@ void decode_kernel(DecParams p) {
         m_s[g] = m_new;
       }
     };
-    if (p.PS <= 16) {
+    if constexpr (MB) {
+      // MFMA phase B. A page's 16 token rows (rows past the context reread the
+      // last valid row; their scores are masked, so p = 0): K in the A-operand
+      // layout of the 16x16x32 product (lane l: token l % 16, elements
+      // 32 c + 8 (l / 16) .. +8), V as consecutive 16-byte chunks (chunk
+      // l + 64 j), written to the wave's LDS slot when the page is folded in.
+      // A wave keeps kBufs pages in flight, as the VALU path below.
+      constexpr int CPR = D / 8;                    // 16-byte chunks per row
+      constexpr int RSH = D == 128 ? 0 : (D == 64 ? 1 : 2);   // log2(rows per 256 bytes)
+      constexpr int kBufs = D == 128 ? 2 : 4;
+      auto vunit = [](int r) { return (r >> RSH) & (D / 16 - 1); };
+      char* vs = vstage[wave];
+      if (wave < nsel) {
+        const int last = wave + ((nsel - 1 - wave) / kDecWaves) * kDecWaves;
+        u32x4_t kr[kBufs][KC], vr[kBufs][KC];
+        auto fetch_mb = [&](int i, u32x4_t (&kx)[KC], u32x4_t (&vx)[KC]) {
+          const int ph = sel_phys[i];
+          const int lp = r0 + (sel_meta[i] & 0xffff);
+          const int valid = min(p.PS, ctx - lp * p.PS);
+          const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvh * p.ks1;
+          const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvh * p.vs1;
+          const int kt = min(t16, valid - 1);
+#pragma unroll
+          for (int c = 0; c < KC; ++c) {
+            kx[c] = *reinterpret_cast<const u32x4_t*>(kpage + kt * p.ks2 + 32 * c + 8 * kg);
+          }
+#pragma unroll
+          for (int j = 0; j < KC; ++j) {
+            const int ci = lane + 64 * j;
+            const int row = min(ci / CPR, valid - 1);
+            vx[j] = *reinterpret_cast<const u32x4_t*>(vpage + row * p.vs2 + 8 * (ci % CPR));
+          }
+        };
+        auto attend_mb = [&](int i, const u32x4_t (&kx)[KC], const u32x4_t (&vx)[KC]) {
+          const int lp = r0 + (sel_meta[i] & 0xffff);
+          const int hmask = sel_meta[i] >> 16;
+          const int valid = min(p.PS, ctx - lp * p.PS);
+#pragma unroll
+          for (int j = 0; j < KC; ++j) {
+            const int ci = lane + 64 * j;
+            const int row = ci / CPR, cc = ci % CPR;
+            *reinterpret_cast<SA_LDS u32x4_t*>((SA_LDS char*)vs + row * 2 * D + 32 * ((cc >> 1) ^ vunit(row)) +
+                                               16 * (cc & 1)) = vx[j];
+          }
+          f32x4_t st = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < KC; ++c) st = Mma16<T>::k32(kx[c], qop[c], st);
+          const bool hsel = (hmask >> t16) & 1;   // lanes of heads >= G: bit clear
+          float s[4];
+          float mloc = -INFINITY;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s[e] = (hsel && 4 * kg + e < valid) ? st[e] * p.qk_scale : -INFINITY;
+            mloc = fmaxf(mloc, s[e]);
+          }
+          mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+          mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+          // O is rescaled only when a head's maximum grows by more than 2^8.
+          if (__any(mloc > mb_m + 8.f)) {
+            const float m_new = fmaxf(mb_m, mloc);
+            const float alpha = fast_exp2(mb_m - (m_new == -INFINITY ? 0.f : m_new));
+            mb_l *= alpha;
+#pragma unroll
+            for (int t = 0; t < DT16; ++t) oacc[t] *= alpha;
+            mb_m = m_new;
+          }
+          const float mref = mb_m == -INFINITY ? 0.f : mb_m;
+          float pe[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pe[e] = fast_exp2(s[e] - mref);
+            mb_l += pe[e];
+          }
+          const u32x2_t pb{Mma16<T>::pack(pe[0], pe[1]), Mma16<T>::pack(pe[2], pe[3])};
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this page's V rows are in LDS
+          // lane l addresses row 4 (l / 16) + (l % 16) / 4, columns 16 t + 4 (l % 4) .. +3, and
+          // receives column 16 t + l % 16 of rows 4 (l / 16) .. +3: V^T in the A layout.
+          const int vr0 = 4 * kg + (t16 >> 2);
+#pragma unroll
+          for (int t = 0; t < DT16; ++t) {
+            SA_LDS s16x4_t* a = (SA_LDS s16x4_t*)((SA_LDS char*)vs + vr0 * 2 * D + 32 * (t ^ vunit(vr0)) +
+                                                  8 * (t16 & 3));
+            const u32x2_t va = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(a));
+            oacc[t] = Mma16<T>::k16(va, pb, oacc[t]);
+          }
+        };
+#pragma unroll
+        for (int b2 = 0; b2 < kBufs - 1; ++b2) fetch_mb(min(wave + b2 * kDecWaves, last), kr[b2], vr[b2]);
+        for (int base = wave; base <= last; base += kBufs * kDecWaves) {
+#pragma unroll
+          for (int b2 = 0; b2 < kBufs; ++b2) {
+            const int i = base + b2 * kDecWaves;
+            if (i > last) break;
+            fetch_mb(min(i + (kBufs - 1) * kDecWaves, last), kr[(b2 + kBufs - 1) % kBufs],
+                     vr[(b2 + kBufs - 1) % kBufs]);
+            attend_mb(i, kr[b2], vr[b2]);
+          }
+        }
+      }
+    } else if (p.PS <= 16) {
       // Whole page per fetch. A wave keeps kDecBufs pages in flight: page
       // i + (kDecBufs-1)*waves is requested before page i is folded in.
       // Fetch indices past the end are clamped to the wave's last page (a
@@ -582,8 +725,24 @@ void decode_kernel(DecParams p) {
   }
 
   // ---- merge lane groups, then waves ---------------------------------------------
+  if constexpr (MB) {
+    float lw = mb_l;
+    lw += __shfl_xor(lw, 16);
+    lw += __shfl_xor(lw, 32);
+    if (t16 < G) {
+      if (kg == 0) {
+        red_m[wave][t16] = mb_m;
+        red_l[wave][t16] = lw;
+      }
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+      for (int t = 0; t < DT16; ++t) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red_acc[wave][t16][16 * t + 4 * kg + e] = oacc[t][e];
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < (MB ? 0 : G); ++g) {
     float mw = fmaxf(m_s[g], __shfl_xor(m_s[g], 16));
     mw = fmaxf(mw, __shfl_xor(mw, 32));
     const float mref = mw == -INFINITY ? 0.f : mw;
@@ -654,14 +813,25 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecParams p) {
   }
 }
 
+template <typename T, int D, int MODE, bool MB>
+void launch_dpm(DecParams& p, dim3 g, hipStream_t s) {
+  switch (p.G) {
+    case 1: hipLaunchKernelGGL((decode_kernel<T, D, 1, MODE, MB>), g, dim3(kDecThreads), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<T, D, 2, MODE, MB>), g, dim3(kDecThreads), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<T, D, 4, MODE, MB>), g, dim3(kDecThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((decode_kernel<T, D, 8, MODE, MB>), g, dim3(kDecThreads), 0, s, p); break;
+  }
+}
+
 template <typename T, int D, int MODE>
 void launch_dp(DecParams& p, dim3 g, hipStream_t s) {
-  switch (p.G) {
-    case 1: hipLaunchKernelGGL((decode_kernel<T, D, 1, MODE>), g, dim3(kDecThreads), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((decode_kernel<T, D, 2, MODE>), g, dim3(kDecThreads), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((decode_kernel<T, D, 4, MODE>), g, dim3(kDecThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((decode_kernel<T, D, 8, MODE>), g, dim3(kDecThreads), 0, s, p); break;
+  if constexpr (sizeof(T) == 2 && (D == 32 || D == 64 || D == 128)) {
+    if (p.mfma_b) {
+      launch_dpm<T, D, MODE, true>(p, g, s);
+      return;
+    }
   }
+  launch_dpm<T, D, MODE, false>(p, g, s);
 }
 
 template <typename T, int D>
@@ -809,6 +979,11 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
   }
   p.os0 = o_strides[0]; p.os1 = o_strides[1]; p.os2 = o_strides[2];
   p.qk_scale = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
+  // MFMA phase B: 16-bit K / V, D in {32, 64, 128}, pages of at most 16
+  // tokens, 16-byte aligned K / V rows (one 16-byte load per lane and row chunk).
+  bool kv16 = (reinterpret_cast<uintptr_t>(k_cache) & 15) == 0 && (reinterpret_cast<uintptr_t>(v_cache) & 15) == 0;
+  for (int i = 0; i < 3; ++i) kv16 = kv16 && (k_strides[i] * esize) % 16 == 0 && (v_strides[i] * esize) % 16 == 0;
+  p.mfma_b = dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128) && page_size <= 16 && kv16;
   hipStream_t s = as_stream(stream);
   if (dtype == SA_DTYPE_F32) return launch_decode<float>(p, s);
   if (dtype == SA_DTYPE_BF16) return launch_decode<bf16_t>(p, s);

@@ -32,6 +32,36 @@ template <> struct Mma<f16_t> {
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
 };
 
+// 16x16 tiles: k32 = v_mfma_f32_16x16x32 (lane l holds 8 consecutive k of
+// row / column l % 16, k-group l / 16), k16 = v_mfma_f32_16x16x16 (4
+// consecutive k per lane). The 16x16 result: lane l holds rows 4 (l / 16) + i,
+// i < 4, of column l % 16.
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4v_t __attribute__((ext_vector_type(4)));
+template <typename T> struct Mma16;
+template <> struct Mma16<bf16_t> {
+  static __device__ __forceinline__ f32x4_t k32(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t k16(u32x2_t a, u32x2_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4v_t, a),
+                                                     __builtin_bit_cast(s16x4v_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+};
+template <> struct Mma16<f16_t> {
+  static __device__ __forceinline__ f32x4_t k32(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t k16(u32x2_t a, u32x2_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a), __builtin_bit_cast(f16x4_t, b), c,
+                                                 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
+};
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt / lgkmcnt left at
 // their "no wait" maxima).
