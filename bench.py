@@ -495,6 +495,19 @@ def main():
             "unique_hbm_bytes": 4 * q.numel() * q.element_size(),
         },
     }
+    # Both roofs for the same launch: config 2's arithmetic intensity (FLOP_alg per
+    # unique HBM byte) sits below the ridge point, so the HBM roof binds first.
+    uniq = 4 * q.numel() * q.element_size()
+    t_mfma_us = flop_alg / (PEAK_BF16_TFLOPS * 1e12) * 1e6
+    t_hbm_us = uniq / (PEAK_HBM_GBS * 1e9) * 1e6
+    result["roofline"]["hbm_view"] = {
+        "achieved_gbs_unique": round(uniq / (fwd_ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(uniq / (fwd_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "intensity_flop_per_byte": round(flop_alg / uniq, 1),
+        "ridge_flop_per_byte": round(PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9), 1),
+        "roof_time_us": {"mfma": round(t_mfma_us, 2), "hbm": round(t_hbm_us, 2)},
+        "frac_of_binding_roof": round(max(t_mfma_us, t_hbm_us) / (fwd_ms * 1e3), 4),
+    }
 
     if args.calibrate_copy:
         # A plain copy of known size: under `rocprofv3 --pmc FETCH_SIZE` / `WRITE_SIZE`

@@ -250,9 +250,10 @@ int sa_block_sparse_bwd_plan(const int32_t* lists, const int32_t* counts, int ma
 /*
  * Workspace bytes needed by sa_sparse_paged_decode for B sequences of H query
  * heads (H_kv kv heads) of dimension D with at most max_pages logical pages
- * each. 0 when B * H_kv work items already fill the GPU, so that each
- * (sequence, kv head) is handled by one workgroup and no split-KV partials
- * are kept; otherwise room for the per-split (max, sum, acc[D]) partials.
+ * each. 0 when the work items already fill the GPU, so that each is handled
+ * by one workgroup and no split-KV partials are kept; otherwise room for the
+ * per-split (max, sum, acc[D]) partials. A work item is a (sequence, kv head)
+ * when the group size H / H_kv is 1, 2, 4 or 8, else a (sequence, query head).
  * No reference counterpart (the reference decode keeps no split-KV partials).
  */
 size_t sa_decode_workspace_bytes(int B, int H, int H_kv, int D, int max_pages);
@@ -262,7 +263,9 @@ size_t sa_decode_workspace_bytes(int B, int H, int H_kv, int D, int max_pages);
  * Replaces: ultrametric_decode / _ultrametric_decode_kernel
  *   (src/ultrametric/kernel_decode.py:188-247 and :22-124), with the CPU
  *   reference semantics for ctx_len <= 0 (zeros, kernel_decode.py:145-152)
- *   and GQA added (k/v caches carry H_kv heads, H % H_kv == 0).
+ *   and GQA added (k/v caches carry H_kv heads, H % H_kv == 0; query head h
+ *   reads kv head h / (H / H_kv); with a group of 1, 2, 4 or 8 heads a K/V page
+ *   is loaded once per group, other group sizes load it per query head).
  *
  * q           (B, H, D); out (B, H, D) — dtype, strides q_strides[3] / o_strides[3].
  * k_cache, v_cache (P, H_kv, page, D) — dtype, strides k_strides[4] / v_strides[4].

@@ -75,6 +75,8 @@ struct DecParams {
   int64_t os0, os1, os2;
   float qk_scale;
   int mfma_b;               // phase B on MFMA (see decode_kernel)
+  int kvdiv;                // work item's kv-head index / kvdiv = the cache head (1, or H / H_kv
+                            // when the group size has no kernel and each query head is its own item)
 };
 
 // DPL consecutive elements (unit stride) kept as raw 32-bit words.
@@ -195,6 +197,7 @@ void decode_kernel(DecParams p) {
   const int bk = work / p.splits;
   const int kvh = bk % p.Hkv;
   const int b = bk / p.Hkv;
+  const int kvm = kvh / p.kvdiv;   // the cache's kv head
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int h0 = kvh * G;
   const int gl = tid % G;       // head (within the group) whose routing vector this lane checks
@@ -543,8 +546,8 @@ void decode_kernel(DecParams p) {
       const int ph = sel_phys[i];
       const int lp = r0 + (sel_meta[i] & 0xffff);
       const int valid = min(p.PS, ctx - lp * p.PS);
-      const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvh * p.ks1 + sub * DPL;
-      const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvh * p.vs1 + sub * DPL;
+      const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvm * p.ks1 + sub * DPL;
+      const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvm * p.vs1 + sub * DPL;
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int tok = min(tc + 4 * it + grp, valid - 1);   // masked rows reread a valid row
@@ -603,8 +606,8 @@ void decode_kernel(DecParams p) {
           const int ph = sel_phys[i];
           const int lp = r0 + (sel_meta[i] & 0xffff);
           const int valid = min(p.PS, ctx - lp * p.PS);
-          const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvh * p.ks1;
-          const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvh * p.vs1;
+          const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvm * p.ks1;
+          const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvm * p.vs1;
           const int kt = min(t16, valid - 1);
 #pragma unroll
           for (int c = 0; c < KC; ++c) {
@@ -873,9 +876,19 @@ int splits_for(int B, int H_kv, int max_pages) {
 }  // namespace
 }  // namespace sa
 
+namespace sa {
+namespace {
+// Work items per sequence: the kv heads when the group size G = H / H_kv has a
+// kernel (1, 2, 4, 8; one item serves the G query heads of a kv head), else the
+// query heads (G = 1 items, each reading kv head h / G).
+bool group_has_kernel(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
+int grid_kv_heads(int H, int H_kv) { return group_has_kernel(H / H_kv) ? H_kv : H; }
+}  // namespace
+}  // namespace sa
+
 extern "C" size_t sa_decode_workspace_bytes(int B, int H, int H_kv, int D, int max_pages) {
-  if (B <= 0 || H <= 0 || H_kv <= 0 || D <= 0) return 0;
-  const int splits = sa::splits_for(B, H_kv, max_pages);
+  if (B <= 0 || H <= 0 || H_kv <= 0 || D <= 0 || H % H_kv != 0) return 0;
+  const int splits = sa::splits_for(B, sa::grid_kv_heads(H, H_kv), max_pages);
   if (splits == 1) return 0;
   return static_cast<size_t>(B) * H * splits * (D + 2) * sizeof(float);
 }
@@ -896,10 +909,9 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
                 size_t workspace_bytes, int dtype, void* stream) {
   using namespace sa;
   if (B < 0 || H < 0 || H_kv <= 0 || (H > 0 && H % H_kv != 0)) return fail(SA_EINVAL, "bad B/H/H_kv");
-  const int G = H > 0 ? H / H_kv : 1;
-  if (G != 1 && G != 2 && G != 4 && G != 8) {
-    return fail(SA_EUNSUPPORTED, "query heads per kv head must be 1, 2, 4 or 8");
-  }
+  const int G_real = H > 0 ? H / H_kv : 1;
+  // Group sizes without a kernel run one work item per query head (G = 1).
+  const int G = group_has_kernel(G_real) ? G_real : 1;
   if (!is_pow2(D) || D < 16 || D > 256) {
     return fail(SA_EUNSUPPORTED, "head_dim must be a power of two in [16, 256]");
   }
@@ -943,11 +955,12 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
   DecParams p{};
   p.q = q; p.kc = k_cache; p.vc = v_cache; p.bt = block_tables; p.ctx = context_lens;
   p.router = router; p.qr = q_router; p.out = out; p.part = static_cast<float*>(workspace);
-  p.B = B; p.H = H; p.Hkv = H_kv; p.D = D; p.PS = page_size; p.TD = TD;
+  p.B = B; p.H = H; p.Hkv = grid_kv_heads(H, H_kv); p.D = D; p.PS = page_size; p.TD = TD;
+  p.kvdiv = group_has_kernel(G_real) ? 1 : G_real;
   p.max_pages = max_pages; p.P = num_phys_pages;
   p.r = req_depth < 0 ? 0 : (req_depth > TD ? TD : req_depth);
   p.local = local_blocks; p.sink = sink_block != 0; p.G = G;
-  p.splits = splits_for(B, H_kv, max_pages);
+  p.splits = splits_for(B, p.Hkv, max_pages);
   if (codes) {
     p.codes = codes;
     p.qcodes = qcodes;

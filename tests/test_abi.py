@@ -56,12 +56,12 @@ def test_host_side_argument_errors():
         rc = lib.sa_block_sparse_fwd(p, p, p, p, None, p, p, None, 0, 1, 1, 1, 64, D, rb, 1, st, st, st, st,
                                      None, 0.1, 1, 0, None)
         assert rc == code, (D, rb)
-    # decode: unsupported GQA group, too small workspace
+    # decode: H not a multiple of H_kv, too small workspace
     st3 = (ctypes.c_int64 * 3)(1, 1, 1)
     st2 = (ctypes.c_int64 * 2)(1, 1)
     stk = (ctypes.c_int64 * 4)(2 * 16 * 64, 16 * 64, 64, 1)
-    args = [p] * 8 + [1, 6, 2, 64, 16, 4, 4, 10, 4, 0, 0, st3, stk, stk, st2, st3, st3, st3, p, 0, 1, None]
-    assert lib.sa_sparse_paged_decode(*args) == nat.SA_EUNSUPPORTED
+    args = [p] * 8 + [1, 7, 2, 64, 16, 4, 4, 10, 4, 0, 0, st3, stk, stk, st2, st3, st3, st3, p, 0, 1, None]
+    assert lib.sa_sparse_paged_decode(*args) == nat.SA_EINVAL
     args[9] = 8
     args[14] = 300  # 300 pages for 2 (sequence, kv head) pairs: split-KV, needs a workspace
     assert lib.sa_sparse_paged_decode(*args) == nat.SA_EINVAL

@@ -63,7 +63,7 @@ def test_reference_grid_fp32(tree_depth):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("H,Hkv", [(4, 4), (8, 2), (32, 8), (8, 1)])
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (8, 2), (32, 8), (8, 1), (6, 2), (10, 2), (28, 4), (32, 2)])
 @pytest.mark.parametrize("D", [64, 128])
 def test_gqa_ragged(dtype, H, Hkv, D):
     args = make(B=5, H=H, Hkv=Hkv, D=D, page=16, pages=80, TD=4, p=2,
