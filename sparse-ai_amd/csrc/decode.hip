@@ -188,6 +188,10 @@ void decode_kernel(DecParams p) {
   // MFMA phase B: one page of V rows per wave (16 rows of 2D bytes), 32-byte
   // units of row r stored at unit u ^ vunit(r).
   __shared__ __attribute__((aligned(16))) char vstage[kDecWaves][MB ? 32 * D : 16];
+  // MFMA phase B: K rows of the wave's early page (16-byte chunk c of row r at
+  // position c ^ (r mod chunks per row)), and the early pages' physical ids.
+  __shared__ __attribute__((aligned(16))) char kstage[kDecWaves][MB ? 32 * D : 16];
+  __shared__ int32_t early_phys[kDecWaves];
 
   // Work items ordered (b, kv head, split); consecutive items (the kv heads of
   // one sequence, which read the same block-table row and router rows) share
@@ -382,13 +386,67 @@ void decode_kernel(DecParams p) {
 #pragma unroll
     for (int g = 0; g < G; ++g) qc[g] = p.qcodes[b * p.qcs0 + (h0 + g) * p.qcs1];
   }
+  // MFMA phase B, split 0: the forced pages need no routing, so up to one per
+  // wave (the sink page, then the last pages of a sequence that fits the first
+  // range) is loaded straight into LDS during phase A and folded in first;
+  // phase A2 leaves them out. Wave 0 takes page 0 when it is the sink, the
+  // next waves take pages n-1, n-2, ...
+  const int e_lim = min(pz, kRange);
+  const int e_s0 = (MB && prefetched && p.sink && n > 0 && e_lim > 0) ? 1 : 0;
+  const int e_m0 = (MB && prefetched && n <= e_lim) ? min(p.local, kDecWaves - e_s0) : 0;
+  const int e_lo = max(n - e_m0, e_s0);   // early local pages: [e_lo, n)
+  auto is_early = [&](int l) { return (e_s0 && l == 0) || (l >= e_lo && l < n); };
+  auto early_wave = [&](int l) { return (e_s0 && l == 0) ? 0 : e_s0 + (n - 1 - l); };
+  int early_l = -1;
+  if (e_s0 && wave == 0) early_l = 0;
+  else if (wave >= e_s0 && n - 1 - (wave - e_s0) >= e_lo) early_l = n - 1 - (wave - e_s0);
+  if constexpr (MB && LOGICAL) {
+    if (prefetched) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int l = 8 * tid + j;
+        if (l < e_lim && is_early(l)) early_phys[early_wave(l)] = lph0[j];
+      }
+    }
+  }
   __syncthreads();
+  if constexpr (MB) {
+    if (early_l >= 0) {
+      const int ph = LOGICAL ? early_phys[wave] : page_phys[early_l];
+      if (ph >= 0 && ph < p.P) {
+        constexpr int CPR = D / 8;
+        constexpr int RSH = D == 128 ? 0 : (D == 64 ? 1 : 2);
+        const int valid = min(p.PS, ctx - early_l * p.PS);
+        const T* kpage = static_cast<const T*>(p.kc) + ph * p.ks0 + kvm * p.ks1;
+        const T* vpage = static_cast<const T*>(p.vc) + ph * p.vs0 + kvm * p.vs1;
+        const uint32_t kdst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SA_LDS char*)kstage[wave]));
+        const uint32_t vdst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((SA_LDS char*)vstage[wave]));
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+          // LDS chunk position 64 i + lane: row r, position pos; fetch the global chunk stored there
+          const int pos_all = 64 * i + lane;
+          const int r = pos_all / CPR, pos = pos_all % CPR;
+          const int rr = min(r, valid - 1);
+          const int kc = pos ^ (r & (CPR - 1));
+          const int vc = 2 * ((pos >> 1) ^ ((r >> RSH) & (D / 16 - 1))) + (pos & 1);
+          dma16(kpage + rr * p.ks2 + 8 * kc, __builtin_amdgcn_readfirstlane(kdst + 1024u * i));
+          dma16(vpage + rr * p.vs2 + 8 * vc, __builtin_amdgcn_readfirstlane(vdst + 1024u * i));
+        }
+      } else {
+        early_l = -1;   // not selected (the page id is out of range)
+      }
+    }
+  }
   int qmine[4] = {0, 0, 0, 0};  // this lane's head's first four query levels (vector path)
   if constexpr (!PACKED && !LOGICAL) {
 #pragma unroll
     for (int lev = 0; lev < 4; ++lev) qmine[lev] = lev < p.r ? qroute[gl][lev] : 0;
   }
 
+  // Phase A's barriers order LDS traffic only: wait for this wave's LDS
+  // accesses, then s_barrier (no fence, which would also wait for the early
+  // pages' direct-to-LDS loads).
+  auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
   for (int r0 = pa; r0 < pz; r0 += kRange) {
     const int r1 = min(pz, r0 + kRange);
     // ---- phase A1: block table + routing vectors -> per-page head mask ---------
@@ -431,7 +489,7 @@ void decode_kernel(DecParams p) {
       load_bt(r0 + kPagesPerThread * tid, ph);
 #pragma unroll
       for (int j = 0; j < kPagesPerThread; ++j) page_phys[kPagesPerThread * tid + j] = ph[j];
-      __syncthreads();
+      lds_barrier();
     }
     for (int hf = 0; hf < kHalves; ++hf) {
     const int hb = r0 + hf * kHalf;                  // first page of this half
@@ -499,7 +557,7 @@ void decode_kernel(DecParams p) {
       }
     }
     }   // halves
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int j = 0; j < kPagesPerThread; ++j) {
       const int l = tid * kPagesPerThread + j;
@@ -507,6 +565,14 @@ void decode_kernel(DecParams p) {
     }
     }
     // ---- phase A2: compact selected pages in ascending logical order -----------
+    if constexpr (MB) {
+      if (r0 == pa && (e_s0 | e_m0)) {
+#pragma unroll
+        for (int j = 0; j < kPagesPerThread; ++j) {
+          if (is_early(r0 + kPagesPerThread * tid + j)) mm[j] = 0;
+        }
+      }
+    }
     int mine = 0;
 #pragma unroll
     for (int j = 0; j < kPagesPerThread; ++j) mine += mm[j] != 0;
@@ -517,7 +583,7 @@ void decode_kernel(DecParams p) {
       if (lane >= off) incl += y;
     }
     if (lane == 63) wave_count[wave] = incl;
-    __syncthreads();
+    lds_barrier();
     int pos = incl - mine, nsel = 0;
 #pragma unroll
     for (int w = 0; w < kDecWaves; ++w) {
@@ -535,7 +601,7 @@ void decode_kernel(DecParams p) {
         ++pos;
       }
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- phase B: gather + attend the selected pages ----------------------------
     // fetch() loads K and V rows of one page into a register buffer; attend()
@@ -599,6 +665,72 @@ void decode_kernel(DecParams p) {
       constexpr int kBufs = D == 128 ? 2 : 4;
       auto vunit = [](int r) { return (r >> RSH) & (D / 16 - 1); };
       char* vs = vstage[wave];
+      // Folds logical page lp (heads in hmask) into the state: K operands in
+      // kx; V rows in vx are first written to the wave's LDS slot when write_v
+      // (the early page's V rows are already there).
+      auto fold = [&](int lp, int hmask, const u32x4_t (&kx)[KC], const u32x4_t (&vx)[KC], bool write_v) {
+        const int valid = min(p.PS, ctx - lp * p.PS);
+        if (write_v) {
+#pragma unroll
+          for (int j = 0; j < KC; ++j) {
+            const int ci = lane + 64 * j;
+            const int row = ci / CPR, cc = ci % CPR;
+            *reinterpret_cast<SA_LDS u32x4_t*>((SA_LDS char*)vs + row * 2 * D + 32 * ((cc >> 1) ^ vunit(row)) +
+                                               16 * (cc & 1)) = vx[j];
+          }
+        }
+        f32x4_t st = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < KC; ++c) st = Mma16<T>::k32(kx[c], qop[c], st);
+        const bool hsel = (hmask >> t16) & 1;   // lanes of heads >= G: bit clear
+        float s[4];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[e] = (hsel && 4 * kg + e < valid) ? st[e] * p.qk_scale : -INFINITY;
+          mloc = fmaxf(mloc, s[e]);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        // O is rescaled only when a head's maximum grows by more than 2^8.
+        if (__any(mloc > mb_m + 8.f)) {
+          const float m_new = fmaxf(mb_m, mloc);
+          const float alpha = fast_exp2(mb_m - (m_new == -INFINITY ? 0.f : m_new));
+          mb_l *= alpha;
+#pragma unroll
+          for (int t = 0; t < DT16; ++t) oacc[t] *= alpha;
+          mb_m = m_new;
+        }
+        const float mref = mb_m == -INFINITY ? 0.f : mb_m;
+        float pe[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pe[e] = fast_exp2(s[e] - mref);
+          mb_l += pe[e];
+        }
+        const u32x2_t pb{Mma16<T>::pack(pe[0], pe[1]), Mma16<T>::pack(pe[2], pe[3])};
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this page's V rows are in LDS
+        // lane l addresses row 4 (l / 16) + (l % 16) / 4, columns 16 t + 4 (l % 4) .. +3, and
+        // receives column 16 t + l % 16 of rows 4 (l / 16) .. +3: V^T in the A layout.
+        const int vr0 = 4 * kg + (t16 >> 2);
+#pragma unroll
+        for (int t = 0; t < DT16; ++t) {
+          SA_LDS s16x4_t* a = (SA_LDS s16x4_t*)((SA_LDS char*)vs + vr0 * 2 * D + 32 * (t ^ vunit(vr0)) +
+                                                8 * (t16 & 3));
+          const u32x2_t va = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(a));
+          oacc[t] = Mma16<T>::k16(va, pb, oacc[t]);
+        }
+      };
+      if (r0 == pa && early_l >= 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the early page's direct-to-LDS loads
+        u32x4_t kx[KC];
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          kx[c] = *reinterpret_cast<SA_LDS u32x4_t*>((SA_LDS char*)kstage[wave] + t16 * 2 * D +
+                                                     16 * ((4 * c + kg) ^ (t16 & (CPR - 1))));
+        }
+        fold(early_l, (1 << G) - 1, kx, kx, false);
+      }
       if (wave < nsel) {
         const int last = wave + ((nsel - 1 - wave) / kDecWaves) * kDecWaves;
         u32x4_t kr[kBufs][KC], vr[kBufs][KC];
@@ -621,57 +753,7 @@ void decode_kernel(DecParams p) {
           }
         };
         auto attend_mb = [&](int i, const u32x4_t (&kx)[KC], const u32x4_t (&vx)[KC]) {
-          const int lp = r0 + (sel_meta[i] & 0xffff);
-          const int hmask = sel_meta[i] >> 16;
-          const int valid = min(p.PS, ctx - lp * p.PS);
-#pragma unroll
-          for (int j = 0; j < KC; ++j) {
-            const int ci = lane + 64 * j;
-            const int row = ci / CPR, cc = ci % CPR;
-            *reinterpret_cast<SA_LDS u32x4_t*>((SA_LDS char*)vs + row * 2 * D + 32 * ((cc >> 1) ^ vunit(row)) +
-                                               16 * (cc & 1)) = vx[j];
-          }
-          f32x4_t st = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < KC; ++c) st = Mma16<T>::k32(kx[c], qop[c], st);
-          const bool hsel = (hmask >> t16) & 1;   // lanes of heads >= G: bit clear
-          float s[4];
-          float mloc = -INFINITY;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            s[e] = (hsel && 4 * kg + e < valid) ? st[e] * p.qk_scale : -INFINITY;
-            mloc = fmaxf(mloc, s[e]);
-          }
-          mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-          mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-          // O is rescaled only when a head's maximum grows by more than 2^8.
-          if (__any(mloc > mb_m + 8.f)) {
-            const float m_new = fmaxf(mb_m, mloc);
-            const float alpha = fast_exp2(mb_m - (m_new == -INFINITY ? 0.f : m_new));
-            mb_l *= alpha;
-#pragma unroll
-            for (int t = 0; t < DT16; ++t) oacc[t] *= alpha;
-            mb_m = m_new;
-          }
-          const float mref = mb_m == -INFINITY ? 0.f : mb_m;
-          float pe[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            pe[e] = fast_exp2(s[e] - mref);
-            mb_l += pe[e];
-          }
-          const u32x2_t pb{Mma16<T>::pack(pe[0], pe[1]), Mma16<T>::pack(pe[2], pe[3])};
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this page's V rows are in LDS
-          // lane l addresses row 4 (l / 16) + (l % 16) / 4, columns 16 t + 4 (l % 4) .. +3, and
-          // receives column 16 t + l % 16 of rows 4 (l / 16) .. +3: V^T in the A layout.
-          const int vr0 = 4 * kg + (t16 >> 2);
-#pragma unroll
-          for (int t = 0; t < DT16; ++t) {
-            SA_LDS s16x4_t* a = (SA_LDS s16x4_t*)((SA_LDS char*)vs + vr0 * 2 * D + 32 * (t ^ vunit(vr0)) +
-                                                  8 * (t16 & 3));
-            const u32x2_t va = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(a));
-            oacc[t] = Mma16<T>::k16(va, pb, oacc[t]);
-          }
+          fold(r0 + (sel_meta[i] & 0xffff), sel_meta[i] >> 16, kx, vx, true);
         };
 #pragma unroll
         for (int b2 = 0; b2 < kBufs - 1; ++b2) fetch_mb(min(wave + b2 * kDecWaves, last), kr[b2], vr[b2]);
