@@ -190,7 +190,10 @@ void decode_kernel(DecParams p) {
   __shared__ __attribute__((aligned(16))) char vstage[kDecWaves][MB ? 32 * D : 16];
   // MFMA phase B: K rows of the wave's early page (16-byte chunk c of row r at
   // position c ^ (r mod chunks per row)), and the early pages' physical ids.
-  __shared__ __attribute__((aligned(16))) char kstage[kDecWaves][MB ? 32 * D : 16];
+  // (Only where the LDS still fits two workgroups per CU: ranges of at most
+  // 2048 pages.)
+  constexpr bool EARLY = MB && kRange <= 2048;
+  __shared__ __attribute__((aligned(16))) char kstage[kDecWaves][EARLY ? 32 * D : 16];
   __shared__ int32_t early_phys[kDecWaves];
 
   // Work items ordered (b, kv head, split); consecutive items (the kv heads of
@@ -392,15 +395,15 @@ void decode_kernel(DecParams p) {
   // phase A2 leaves them out. Wave 0 takes page 0 when it is the sink, the
   // next waves take pages n-1, n-2, ...
   const int e_lim = min(pz, kRange);
-  const int e_s0 = (MB && prefetched && p.sink && n > 0 && e_lim > 0) ? 1 : 0;
-  const int e_m0 = (MB && prefetched && n <= e_lim) ? min(p.local, kDecWaves - e_s0) : 0;
+  const int e_s0 = (EARLY && prefetched && p.sink && n > 0 && e_lim > 0) ? 1 : 0;
+  const int e_m0 = (EARLY && prefetched && n <= e_lim) ? min(p.local, kDecWaves - e_s0) : 0;
   const int e_lo = max(n - e_m0, e_s0);   // early local pages: [e_lo, n)
   auto is_early = [&](int l) { return (e_s0 && l == 0) || (l >= e_lo && l < n); };
   auto early_wave = [&](int l) { return (e_s0 && l == 0) ? 0 : e_s0 + (n - 1 - l); };
   int early_l = -1;
   if (e_s0 && wave == 0) early_l = 0;
   else if (wave >= e_s0 && n - 1 - (wave - e_s0) >= e_lo) early_l = n - 1 - (wave - e_s0);
-  if constexpr (MB && LOGICAL) {
+  if constexpr (EARLY && LOGICAL) {
     if (prefetched) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -410,7 +413,7 @@ void decode_kernel(DecParams p) {
     }
   }
   __syncthreads();
-  if constexpr (MB) {
+  if constexpr (EARLY) {
     if (early_l >= 0) {
       const int ph = LOGICAL ? early_phys[wave] : page_phys[early_l];
       if (ph >= 0 && ph < p.P) {
@@ -721,7 +724,7 @@ void decode_kernel(DecParams p) {
           oacc[t] = Mma16<T>::k16(va, pb, oacc[t]);
         }
       };
-      if (r0 == pa && early_l >= 0) {
+      if (EARLY && r0 == pa && early_l >= 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the early page's direct-to-LDS loads
         u32x4_t kx[KC];
 #pragma unroll

@@ -106,9 +106,19 @@ __device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t
 template <int LPW, int MAXA>
 __device__ __forceinline__ void wait_tiles(int ahead) {
   static_assert(MAXA >= 1 && MAXA <= 3, "pipeline depth");
-  if (MAXA >= 3 && ahead >= 3) wait_vmcnt<3 * LPW>();
-  else if (MAXA >= 2 && ahead >= 2) wait_vmcnt<2 * LPW>();
-  else if (ahead >= 1) wait_vmcnt<LPW>();
+  if constexpr (MAXA >= 3) {
+    if (ahead >= 3) {
+      wait_vmcnt<3 * LPW>();
+      return;
+    }
+  }
+  if constexpr (MAXA >= 2) {
+    if (ahead >= 2) {
+      wait_vmcnt<2 * LPW>();
+      return;
+    }
+  }
+  if (ahead >= 1) wait_vmcnt<LPW>();
   else wait_vmcnt<0>();
 }
 

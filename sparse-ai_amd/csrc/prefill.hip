@@ -9,7 +9,7 @@
 // element type before the PV product, as the reference does (p.to(v.dtype)).
 //
 // Two kernels:
-//  * prefill_mfma_kernel — bf16/fp16, D in {32, 64, 128}, route_block % 32 == 0.
+//  * prefill_mfma_kernel — bf16/fp16, D in {32, 64, 128, 256}, route_block % 32 == 0.
 //    A workgroup of NW waves owns BM = 32*NW query rows of one route block;
 //    Q stays in registers as MFMA operands. Each wave computes S^T = K Q^T on
 //    32x32x16 MFMA tiles, so lane (i + 32h) holds 16 keys of query i per
@@ -202,7 +202,7 @@ void prefill_mfma_kernel(FwdParams p) {
   constexpr int DT = D / 32;           // 32-row O^T tiles
   constexpr int NKI = TILEB / 1024;    // 1-KB direct-to-LDS loads per K tile
   constexpr int LPW = 2 * NKI / NW;    // loads per wave per stage (K and V)
-  constexpr int RSH = D == 128 ? 0 : (D == 64 ? 1 : 2);  // log2(rows per 256 B)
+  constexpr int RSH = D >= 128 ? 0 : (D == 64 ? 1 : 2);  // log2(rows per 256 B), 0 for rows of 256 B or more
   static_assert((2 * NKI) % NW == 0, "loads must split evenly over waves");
   static_assert(S >= 3 && S <= 4, "pipeline stages");
   // O is rescaled only when a row maximum grows by more than this (log2
@@ -266,7 +266,7 @@ void prefill_mfma_kernel(FwdParams p) {
   //      bytes of a 32-lane one land in distinct banks of a 128-byte and of
   //      a 256-byte bank window alike.
   auto fk = [](int r) { return (r >> RSH) & (CPR - 1); };
-  auto vsig = [](int r) { return D == 128 ? (r & 3) : (D == 64 ? ((r >> 1) & 1) : 0); };
+  auto vsig = [](int r) { return D >= 128 ? (r & 3) : (D == 64 ? ((r >> 1) & 1) : 0); };
   auto vtau = [](int r) { return D == 64 ? (r & 1) : ((r >> 1) & 1); };
   auto fv = [&](int r) { return 4 * vsig(r) + 2 * vtau(r); };
 
@@ -608,7 +608,13 @@ void launch_mfma_shape(FwdParams& p, hipStream_t stream) {
 // prologue / epilogue latency overlaps the others' MFMA work.
 template <typename T, int D, int NW>
 void launch_mfma_variant(FwdParams& p, hipStream_t stream) {
-  launch_mfma_shape<T, D, NW, 3, 3>(p, stream);
+  if constexpr (D == 256) {
+    // Q (64 registers) and O (128) of a 32-row slice: one wave per SIMD, one
+    // workgroup per CU (three 32 KB stages).
+    launch_mfma_shape<T, D, NW, 3, 1>(p, stream);
+  } else {
+    launch_mfma_shape<T, D, NW, 3, 3>(p, stream);
+  }
 }
 
 template <typename T, int D>
@@ -616,7 +622,7 @@ int launch_mfma_d(FwdParams& p, hipStream_t stream) {
   const int RB = p.RB;
   if (RB % 128 == 0) launch_mfma_variant<T, D, 4>(p, stream);
   else if (RB == 64) launch_mfma_variant<T, D, 2>(p, stream);
-  else launch_mfma_variant<T, D, 1>(p, stream);  // RB == 32
+  else if constexpr (D != 256) launch_mfma_variant<T, D, 1>(p, stream);  // RB == 32 (D = 256 needs RB >= 64)
   return check_launch("block-sparse prefill (MFMA) kernel");
 }
 
@@ -625,6 +631,7 @@ int launch_mfma(FwdParams& p, int D, hipStream_t stream) {
   switch (D) {
     case 32: return launch_mfma_d<T, 32>(p, stream);
     case 64: return launch_mfma_d<T, 64>(p, stream);
+    case 256: return launch_mfma_d<T, 256>(p, stream);
     default: return launch_mfma_d<T, 128>(p, stream);
   }
 }
@@ -707,7 +714,7 @@ int fwd_impl(const void* q, const void* k, const void* v, void* out, float* lse,
   const long long max_rs = std::max({p.qs2, p.ks2, p.vs2}) * 2;
   const bool offs_ok = N < (1 << 24) && max_rs < (1 << 24) &&
                        static_cast<long long>(N) * max_rs < (1LL << 32);
-  const bool mfma_ok = dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128) &&
+  const bool mfma_ok = dtype != SA_DTYPE_F32 && (D == 32 || D == 64 || D == 128 || (D == 256 && route_block >= 64)) &&
                        route_block >= 32 && rows_ok && offs_ok;
   const long long wg = static_cast<long long>(Z) * H * ((N + 15) / 16);
   if (wg > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");

@@ -63,7 +63,7 @@ KERNEL_CASES = [
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("N,rb,depth,is_causal,sink,local", KERNEL_CASES)
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_kernel_matches_oracle(dtype, N, rb, depth, is_causal, sink, local, D):
     Z, H = 1, 2
     q, k, v = inputs(Z, H, N, D, dtype, seed=N + D)
@@ -81,7 +81,7 @@ def test_kernel_matches_oracle(dtype, N, rb, depth, is_causal, sink, local, D):
     assert torch.equal(out, out2)  # storing LSE does not change out
 
 
-@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_head_dims_reference_shape(head_dim, dtype):
     Z, H, N, rb = 1, 4, 2048, 128
