@@ -18,6 +18,8 @@
 // kernel, so the output needs no memset.
 #include "sa_internal.h"
 
+#include <algorithm>
+
 namespace sa {
 namespace {
 
@@ -238,35 +240,41 @@ extern "C" int sa_build_block_lists_mask(const uint8_t* mask, const int64_t* mas
 namespace sa {
 namespace {
 
-constexpr int kTransMaxNB = 512;   // bit matrix of NB x NB bits (+ padding) in 34 KB of LDS
+// Bit matrix of the transpose: CK key-block rows of NB query-block bits (odd
+// row stride in words, so that the row scans below do not share banks), at
+// most 64 KB of dynamic LDS; NB up to kMaxNB.
+constexpr int kTransLdsWords = 16384;
 
-// One workgroup per (z, h): every listed pair (qb, kb) sets bit qb of row kb
-// of an LDS bit matrix (row stride odd, so the row scans below do not share
-// banks); thread kb then writes row kb's query blocks in ascending order,
-// zero-padded to t_cols, and its count.
+// One workgroup per (z, h, chunk of CK key blocks): every listed pair
+// (qb, kb) with kb in the chunk sets bit qb of row kb - k0; thread j then
+// writes row k0 + j's query blocks in ascending order, zero-padded to t_cols,
+// and its count. Every chunk scans all of the head's list entries, so a grid
+// of NB <= 512 is one chunk per head.
 __global__ __launch_bounds__(1024) void transpose_lists_kernel(const int32_t* lists, const int32_t* counts,
-                                                               int max_count, int NB, int32_t* t_lists,
-                                                               int t_cols, int32_t* t_counts) {
-  __shared__ uint32_t bits[kTransMaxNB * (kTransMaxNB / 32 + 1)];
-  const int zh = blockIdx.x, tid = threadIdx.x;
+                                                               int max_count, int NB, int CK, int chunks,
+                                                               int32_t* t_lists, int t_cols, int32_t* t_counts) {
+  extern __shared__ uint32_t bits[];
+  const int zh = blockIdx.x / chunks, k0 = (blockIdx.x % chunks) * CK, tid = threadIdx.x;
+  const int nk = min(CK, NB - k0);
   const int W = (NB + 31) / 32, WS = W | 1;
-  for (int i = tid; i < NB * WS; i += 1024) bits[i] = 0u;
+  for (int i = tid; i < nk * WS; i += 1024) bits[i] = 0u;
   __syncthreads();
   const int32_t* L = lists + static_cast<int64_t>(zh) * NB * max_count;
   const int32_t* C = counts + static_cast<int64_t>(zh) * NB;
-  for (int i = tid; i < NB * max_count; i += 1024) {
-    const int qb = i / max_count, t = i % max_count;
+  for (int64_t i = tid; i < static_cast<int64_t>(NB) * max_count; i += 1024) {
+    const int qb = static_cast<int>(i / max_count), t = static_cast<int>(i % max_count);
     if (t < min(max(C[qb], 0), max_count)) {
-      const int kb = L[i];
-      if (kb >= 0 && kb < NB) atomicOr(&bits[kb * WS + (qb >> 5)], 1u << (qb & 31));
+      const int kb = L[i] - k0;
+      if (kb >= 0 && kb < nk) atomicOr(&bits[kb * WS + (qb >> 5)], 1u << (qb & 31));
     }
   }
   __syncthreads();
-  for (int kb = tid; kb < NB; kb += 1024) {
+  for (int j = tid; j < nk; j += 1024) {
+    const int kb = k0 + j;
     int n = 0;
     int32_t* out = t_lists ? t_lists + (static_cast<int64_t>(zh) * NB + kb) * t_cols : nullptr;
     for (int w = 0; w < W; ++w) {
-      uint32_t x = bits[kb * WS + w];
+      uint32_t x = bits[j * WS + w];
       while (x) {
         const int b = __builtin_ctz(x);
         x &= x - 1u;
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(1024) void transpose_lists_kernel(const int32_t* li
       }
     }
     if (out) {
-      for (int j = n; j < t_cols; ++j) out[j] = 0;
+      for (int c = n; c < t_cols; ++c) out[c] = 0;
     }
     t_counts[static_cast<int64_t>(zh) * NB + kb] = n;
   }
@@ -288,13 +296,17 @@ extern "C" int sa_transpose_block_lists(const int32_t* lists, const int32_t* cou
                                         int NB, int32_t* t_lists, int t_cols, int32_t* t_counts, void* stream) {
   using namespace sa;
   if (Z < 0 || H < 0 || NB < 0 || max_count < 0 || t_cols < 0) return fail(SA_EINVAL, "negative size");
-  if (NB > kTransMaxNB) return fail(SA_EUNSUPPORTED, "transposed lists need NB <= 512");
+  if (NB > kMaxNB) return fail(SA_EUNSUPPORTED, "transposed lists need NB <= " + std::to_string(kMaxNB));
   const long long zh = static_cast<long long>(Z) * H;
   if (zh == 0 || NB == 0) return SA_OK;
   if (!counts || !t_counts || (max_count > 0 && !lists)) return fail(SA_EINVAL, "NULL tensor argument");
   if (t_lists && t_cols < 1) return fail(SA_EINVAL, "t_cols must be >= 1 when t_lists is given");
-  if (zh > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
-  hipLaunchKernelGGL(transpose_lists_kernel, dim3(static_cast<unsigned>(zh)), dim3(1024), 0, as_stream(stream),
-                     lists, counts, max_count, NB, t_lists, t_cols, t_counts);
+  const int WS = ((NB + 31) / 32) | 1;
+  const int CK = std::min(NB, kTransLdsWords / WS);
+  const int chunks = (NB + CK - 1) / CK;
+  if (zh * chunks > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
+  hipLaunchKernelGGL(transpose_lists_kernel, dim3(static_cast<unsigned>(zh * chunks)), dim3(1024),
+                     static_cast<size_t>(CK) * WS * sizeof(uint32_t), as_stream(stream), lists, counts, max_count,
+                     NB, CK, chunks, t_lists, t_cols, t_counts);
   return check_launch("block-list transpose kernel");
 }

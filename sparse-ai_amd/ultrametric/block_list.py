@@ -270,7 +270,7 @@ def build_transposed_block_lists(
     return block_lists_from_mask(match_kq, sync_free=False)
 
 
-_TRANSPOSE_MAX_NB = 512   # sa_transpose_block_lists limit; larger grids use torch scatter + compaction
+_TRANSPOSE_MAX_NB = 8192  # sa_transpose_block_lists limit (the builder's); larger grids use torch scatter + compaction
 
 
 def _launch_transpose(lists, counts, max_count, t_lists, t_cols, t_counts):

@@ -135,9 +135,11 @@ def test_empty_and_dense_edges():
     assert build_block_lists(r, 0, is_causal=True).counts[0, 0].tolist() == [1, 2, 3, 4, 5]
 
 
-@pytest.mark.parametrize("NB,density", [(33, 0.3), (300, 0.05), (512, 0.02), (600, 0.01)])
+@pytest.mark.parametrize("NB,density", [(33, 0.3), (300, 0.05), (512, 0.02), (600, 0.01), (1200, 0.004),
+                                        (2100, 0.002)])
 def test_transposed_lists_large(NB, density):
-    # the HIP transpose kernel (NB <= 512) and the scatter path above it
+    # the HIP transpose kernel: one key-block chunk per head up to NB = 512,
+    # several chunks above (431 key blocks per chunk at NB = 1200, 244 at 2100)
     rng = np.random.default_rng(NB + 1)
     mask = rng.random((1, 2, NB, NB)) < density
     mask[..., 0] = True                       # a full sink column
