@@ -21,10 +21,14 @@ block-list kernel in the reference, as free functions over the same inputs
   surgery.py:589-595.
 
 Gradients with respect to q, k and v flow through block_list_attention's
-backward. The router's straight-through soft-bias term (surgery.py:566-588)
-is built from the model's expected block distances; a caller that has them
-passes the resulting bias to block_list_attention (``soft_block_bias``), whose
-backward returns its gradient.
+backward. When grad is enabled and the routing scores require grad, the
+router's straight-through soft-bias term is built as the reference does
+(surgery.py:566-588): block-mean assignments, their expected tree distance
+(``expected_block_distance``, topology.py:456-485), soft logits
+(max_dist - distance) / 0.5 gathered at each row's listed blocks, and the
+zero-valued bias g - g.detach() passed to block_list_attention as
+``soft_block_bias``; the kernel's backward returns its gradient, which
+autograd carries to the scores.
 """
 
 from __future__ import annotations
@@ -36,7 +40,8 @@ import torch
 from . import _native as nat
 from .block_list import block_list_attention, build_block_lists
 
-__all__ = ["route_block_vote", "block_list_prefill", "local_blocks_of", "RouteCache"]
+__all__ = ["route_block_vote", "block_list_prefill", "local_blocks_of", "RouteCache", "expected_block_distance",
+           "ste_soft_block_bias"]
 
 _SCORE_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -44,6 +49,62 @@ _SCORE_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 def local_blocks_of(local_window: int, route_block: int) -> int:
     """Local band in blocks for a token window (surgery.py:550-551)."""
     return -(-int(local_window) // int(route_block)) if local_window > 0 else 0
+
+
+def expected_block_distance(block_assignments: torch.Tensor, p: int = 2) -> torch.Tensor:
+    """(B, H, NB, L, p) soft branch probabilities -> (B, H, NB, NB) expected tree
+    distance (topology.py:456-485): with m_l(i, j) = sum_p a_i[l, p] a_j[l, p] the
+    chance that blocks i and j take the same branch at level l, the chance that
+    they share levels 0..l is taken as min(m_0, ..., m_l), and the distance is
+    L minus the sum of those over l. When the input requires grad, the backward
+    also sees a tie-breaking term 0.05 * 2^(l - (L - 1)) * m_l per level (its
+    forward value cancels), as the reference adds. ``p`` is the arity (the
+    last dimension); the formula does not otherwise use it."""
+    if block_assignments.dim() != 5:
+        raise ValueError(f"block_assignments must be (B, H, NB, L, p); got {tuple(block_assignments.shape)}")
+    a = block_assignments
+    L = a.shape[-2]
+    # (B, H, L, NB, p) @ (B, H, L, p, NB) -> m[b, h, l, i, j], in the input's precision
+    al = a.permute(0, 1, 3, 2, 4).contiguous()
+    m = torch.matmul(al, al.transpose(-1, -2).contiguous())
+    m = m.permute(0, 1, 3, 4, 2)                                  # (B, H, NB, NB, L)
+    shared = torch.cummin(m, dim=-1).values
+    if m.requires_grad:
+        w = 0.05 * torch.pow(2.0, torch.arange(L, device=m.device, dtype=m.dtype) - (L - 1))
+        tie = m * w
+        shared = shared + (tie - tie.detach())
+    return L - shared.sum(dim=-1)
+
+
+def _block_mean(assignments: torch.Tensor, S: int, route_block: int) -> torch.Tensor:
+    """(B, H, S, L, p) -> (B, H, NB, L, p): the mean over each route block's tokens
+    (a last block shorter than route_block averages its valid tokens only)."""
+    B, H, _, L, P = assignments.shape
+    NB = -(-S // route_block)
+    a = assignments[:, :, :S]
+    pad = NB * route_block - S
+    if pad:
+        a = torch.cat([a, a.new_zeros(B, H, pad, L, P)], dim=2)
+    n = torch.full((NB,), float(route_block), dtype=a.dtype, device=a.device)
+    n[-1] = S - (NB - 1) * route_block
+    return a.view(B, H, NB, route_block, L, P).sum(dim=3) / n.view(1, 1, NB, 1, 1)
+
+
+def ste_soft_block_bias(block_assignments: torch.Tensor, lists: torch.Tensor, r: int, p: int,
+                        max_dist: Optional[float] = None) -> torch.Tensor:
+    """The router's straight-through soft bias (surgery.py:577-588): logits
+    (max_dist - expected_block_distance) / 0.5 gathered at each row's listed
+    blocks (entries clamped into [0, NB)), returned as g - g.detach(): zero in
+    the forward pass, gradient 1 with respect to g. ``max_dist`` defaults to
+    L - r, as the reference's config default."""
+    L = block_assignments.shape[-2]
+    NB = block_assignments.shape[2]
+    md = float(max_dist) if max_dist is not None else float(L - int(r))
+    dist = expected_block_distance(block_assignments.float(), p=p)
+    logits = (md - dist) / 0.5
+    idx = lists.clamp(min=0, max=max(NB - 1, 0)).to(torch.int64)
+    g = torch.gather(logits, dim=-1, index=idx)
+    return g - g.detach()
 
 
 def route_block_vote(assignments: torch.Tensor, r: int, route_block: int) -> torch.Tensor:
@@ -103,7 +164,7 @@ def block_list_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, assign
                        *, p: int, route_block: int = 128, local_window: int = 16,
                        sm_scale: Optional[float] = None, block_assignments: Optional[torch.Tensor] = None,
                        return_stats: bool = False, route_cache: Optional[RouteCache] = None,
-                       layer_idx: Optional[int] = None):
+                       layer_idx: Optional[int] = None, max_dist: Optional[float] = None):
     """Causal block-list prefill with block-granular tree routing.
 
     q: (B, H, S, D); k, v: (B, H_kv, S, D). ``assignments``: (B, H, S, L, p)
@@ -114,7 +175,10 @@ def block_list_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, assign
     ``mean_allowed_keys``, ``mean_causal_keys`` and ``block_density``
     (surgery.py:589-595; host reads) when ``return_stats``. With ``route_cache``
     and ``layer_idx``, non-anchor layers reuse their anchor's lists (see
-    RouteCache) and ``assignments`` is not read for them.
+    RouteCache) and ``assignments`` is not read for them. When grad is
+    enabled and ``assignments`` requires grad, the straight-through soft bias
+    (``ste_soft_block_bias``, ``max_dist`` defaulting to L - r) is added, so
+    the scores receive the reference's router gradient (surgery.py:566-588).
     """
     B, H, S, _ = q.shape
     RB = int(route_block)
@@ -138,7 +202,17 @@ def block_list_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, assign
                                local_blocks=local_blocks_of(local_window, RB), arity=p)
         if route_cache is not None and layer_idx is not None:
             route_cache.store(int(layer_idx), key, bl)
-    out = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True, sm_scale=sm_scale)
+    soft_bias = None
+    if torch.is_grad_enabled() and assignments is not None and assignments.requires_grad:
+        if block_assignments is not None and block_assignments.shape[2] == NB:
+            blk = block_assignments[:, :, :NB]
+        elif assignments.shape[2] == NB and NB != S:
+            blk = assignments[:, :, :NB]
+        else:
+            blk = _block_mean(assignments, S, RB)
+        soft_bias = ste_soft_block_bias(blk, bl.lists, r, p, max_dist=max_dist)
+    out = block_list_attention(q, k, v, bl, route_block=RB, is_causal=True, sm_scale=sm_scale,
+                               soft_block_bias=soft_bias)
     if not return_stats:
         return out
     lens = torch.full((NB,), RB, dtype=torch.float32, device=q.device)

@@ -155,3 +155,53 @@ def test_block_list_prefill_config5_layer():
     # earlier blocks; with the diagonal, sink and one local block that is
     # about 10% of the 8256 causal blocks per head
     assert 0.05 < st["block_density"] < 0.15
+
+
+def _dense_with_block_bias(q, k, v, lists, counts, bias, rb, scale):
+    """Token-level masked attention in float32 (torch on the GPU) with the
+    per-(query block, list slot) bias added to that pair's scores."""
+    Z, H, S, D = q.shape
+    NB = counts.shape[-1]
+    slot = torch.arange(lists.shape[-1], device=q.device).view(1, 1, 1, -1) < counts.unsqueeze(-1)
+    kb = lists.clamp(0, NB - 1).long()
+    # padding entries (kb 0, slot False) share index 0 with the sink: add, do not overwrite
+    allowed = torch.zeros(Z, H, NB, NB, dtype=torch.int32, device=q.device).scatter_add(-1, kb, slot.int()) > 0
+    bfull = torch.zeros(Z, H, NB, NB, dtype=torch.float32, device=q.device).scatter_add(
+        -1, kb, torch.where(slot, bias, torch.zeros_like(bias)))
+    tok = torch.arange(S, device=q.device) // rb
+    m = allowed[:, :, tok][:, :, :, tok] & (torch.arange(S, device=q.device).view(-1, 1)
+                                           >= torch.arange(S, device=q.device).view(1, -1))
+    s = torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale + bfull[:, :, tok][:, :, :, tok]
+    s = s.masked_fill(~m, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), v)
+
+
+def test_router_gradient_through_the_straight_through_bias():
+    # block_list_prefill with scores that require grad adds the zero-valued STE
+    # bias (surgery.py:566-588); the scores' gradient through the kernel's
+    # soft-bias backward equals the one through dense masked attention with the
+    # same bias (float32 inputs: the fp32 kernels)
+    from ultrametric import build_block_lists
+    from ultrametric.surgery import _block_mean, ste_soft_block_bias, local_blocks_of
+    B, H, S, D, rb, L, p, r = 1, 2, 300, 64, 64, 3, 4, 2
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn(B, H, S, D, generator=g).to(DEV) for _ in range(3))
+    scores = torch.randn(B, H, S, L, p, generator=g).to(DEV)
+    a1 = torch.softmax(scores, -1).detach().requires_grad_(True)
+    a2 = a1.detach().clone().requires_grad_(True)
+    dout = torch.randn(B, H, S, D, generator=g).to(DEV)
+    scale = 1.0 / math.sqrt(D)
+    out = block_list_prefill(q, k, v, a1, r, p=p, route_block=rb, local_window=16, sm_scale=scale)
+    with torch.no_grad():
+        out_ng = block_list_prefill(q, k, v, a1, r, p=p, route_block=rb, local_window=16, sm_scale=scale)
+    assert torch.equal(out, out_ng)                    # the bias is zero in the forward pass
+    out.backward(dout)
+    route = route_block_vote(a2.detach(), r, rb)
+    bl = build_block_lists(route, r, is_causal=True, sink_block=True, local_blocks=local_blocks_of(16, rb), arity=p)
+    bias = ste_soft_block_bias(_block_mean(a2, S, rb), bl.lists, r, p)
+    ref = _dense_with_block_bias(q, k, v, bl.lists, bl.counts, bias, rb, scale)
+    assert torch.allclose(out, ref, atol=1e-4, rtol=0)
+    ref.backward(dout)
+    assert a1.grad.abs().max() > 0
+    err = (a1.grad - a2.grad).abs().max() / a2.grad.abs().max()
+    assert err <= 1e-4, err
