@@ -2,7 +2,8 @@
 tests cover one at a time: prefill with GQA, soft block bias, LSE, per-head
 routing depths, ragged sequence lengths, every route block and head dim the
 kernels take, causal / sink / local masks, and strided inputs; the backward on
-the same kind of cases; decode with random page sizes, group sizes, depths,
+the same kind of cases; decode with random page sizes, group sizes (1, 2, 4,
+8, and sizes without a kernel of their own: 3, 5, 6, 7, 16), depths,
 ragged and empty contexts, through the int32 router and the packed-code
 entry; the fused routed prefill (list build inside the forward kernel), bit
 for bit against the two-launch path. Every case, the fused ones included,
@@ -194,6 +195,29 @@ def test_decode_random_combination(c):
     pc, qc = pack_routing_codes(r.to(DEV), 1), pack_routing_codes(qr.to(DEV), 1)
     outp = ultrametric_decode_packed(*(t.to(DEV) for t in (q, kc, vc, bt, ctx)), pc, qc, TD, 1, **kw)
     assert torch.equal(outp, out)
+
+
+def _dec_cases_groups(n):
+    # group sizes without a kernel of their own (one work item per query head)
+    rng = np.random.default_rng(77)
+    cases = []
+    for i in range(n):
+        page = int(rng.choice([8, 16]))
+        G = int(rng.choice([3, 5, 6, 7, 16]))
+        Hkv = int(rng.choice([1, 2]))
+        B = int(rng.integers(1, 5))
+        lens = [int(rng.choice([0, 1, int(rng.integers(1, 40 * page))])) for _ in range(B)]
+        cases.append(dict(i=i, dtype=DTYPES[int(rng.integers(0, 3))], page=page, H=Hkv * G, Hkv=Hkv,
+                          D=int(rng.choice([64, 128])), B=B, lens=lens, TD=int(rng.integers(1, 5)),
+                          depth=int(rng.integers(0, 6)), local=int(rng.integers(0, 3)),
+                          sink=bool(rng.integers(0, 2)), seed=int(rng.integers(0, 1 << 30))))
+    return cases
+
+
+@pytest.mark.parametrize("c", _dec_cases_groups(16),
+                         ids=lambda c: f"{c['i']}-{str(c['dtype'])[6:]}-pg{c['page']}-H{c['H']}/{c['Hkv']}-D{c['D']}")
+def test_decode_random_group_sizes(c):
+    test_decode_random_combination(c)
 
 
 def _fused_cases(n):
