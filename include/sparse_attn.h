@@ -238,7 +238,9 @@ int sa_block_sparse_bwd(const void* q, const void* k, const void* v, const void*
  * receiving {work items, split tiles, work items of split tiles}; the caller
  * reads it back (one device-to-host copy, at the point where the reference
  * reads max(q_counts)) to size the launch and dkv_partials.
- * With soft_bias the plan also holds each transposed entry's bias.
+ * With soft_bias the plan also holds each transposed entry's bias. The plan
+ * also resolves every work item's entries (first query row, head, bias), so
+ * the work that follows the read-back is the dK / dV kernels alone.
  */
 size_t sa_block_sparse_bwd_plan_bytes(int Z, int H, int H_kv, int N, int route_block, int t_max_count);
 int sa_block_sparse_bwd_plan(const int32_t* lists, const int32_t* counts, int max_count,

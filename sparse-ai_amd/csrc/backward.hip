@@ -310,7 +310,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdParams p) {
 //       `chunk` transposed-list entries; the items of a key tile with more
 //       entries write fp32 partials that bwd_finalize_kernel sums.
 //   bwd_plan_kernel      — builds the work list (split tiles first, then the
-//       others by decreasing entry count) from the transposed counts.
+//       others by decreasing entry count) from the transposed counts;
+//       bwd_items_kernel then resolves each item's entries.
 // ============================================================================
 constexpr int kBwdSeg = 256;        // dQ: list entries staged in LDS at a time
 constexpr int kChunkStages = 32;    // dK/dV: 32-row query stages per work item
@@ -722,17 +723,12 @@ __global__ __launch_bounds__(256) void bwd_tbias_kernel(BwdParams p, float* t_bi
   if (lo < tc && tl[lo] == qb) t_bias[trow * p.t_max + lo] = bias_at(p, zh / p.H, zh % p.H, qb, t);
 }
 
-// PASS 0 accumulates dV (S, P, dV^T += dO^T P; K in registers), PASS 1 dK
-// (S, dP, dS, dK^T += Q^T dS; K and V in registers): one pass holding K, V
-// and both fp32 accumulators would not fit two waves per SIMD at D = 128.
 // Resolves the transposed entries of each work item once (lane e: entry
 // chunk * C + e, walked over the G query heads of the kv head), so that the
-// dK / dV workgroups load them with one read.
-__global__ __launch_bounds__(64) void bwd_items_kernel(BwdParams p) {
-  const int w = blockIdx.x, e = threadIdx.x;
-  const int4 item = p.work[w];
-  const int ne = max(0, min(item.w - item.y * p.chunk, p.chunk));
-  if (e >= ne) return;
+// dK / dV workgroups load them with one read. Part of the plan: it runs
+// before the item count is read back, so it walks the items up to info[0]
+// with a fixed grid, one wave per item.
+__device__ __forceinline__ void resolve_entry(const BwdParams& p, int4 item, int w, int e) {
   const int zk = item.x / p.ktiles, nt = item.x % p.ktiles;
   const int z = zk / p.Hkv, kvh = zk % p.Hkv;
   const int kb = nt * p.key_tile / p.RB;
@@ -751,6 +747,18 @@ __global__ __launch_bounds__(64) void bwd_items_kernel(BwdParams p) {
   p.ent_b[slot] = p.t_bias ? p.t_bias[trow * p.t_max + u] : 0.f;
 }
 
+__global__ __launch_bounds__(256) void bwd_items_kernel(BwdParams p, const int32_t* info) {
+  const int n_items = info[0], e = threadIdx.x & 63;
+  for (int w = blockIdx.x * 4 + (threadIdx.x >> 6); w < n_items; w += gridDim.x * 4) {
+    const int4 item = p.work[w];
+    const int ne = max(0, min(item.w - item.y * p.chunk, p.chunk));
+    if (e < ne) resolve_entry(p, item, w, e);
+  }
+}
+
+// PASS 0 accumulates dV (S, P, dV^T += dO^T P; K in registers), PASS 1 dK
+// (S, dP, dS, dK^T += Q^T dS; K and V in registers): one pass holding K, V
+// and both fp32 accumulators would not fit two waves per SIMD at D = 128.
 template <typename T, int D, int NW, bool CAUSAL, int PASS>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(PASS == 0 ? 3 : 2)))
 void bwd_dkdv_mfma_kernel(BwdParams p) {
@@ -983,9 +991,6 @@ int launch_dq_mfma_nw(BwdParams& p, hipStream_t s) {
 template <typename T, int D, int NW>
 int launch_dkdv_mfma_nw(BwdParams& p, hipStream_t s) {
   if (p.n_work == 0) return SA_OK;
-  hipLaunchKernelGGL(bwd_items_kernel, dim3(p.n_work), dim3(64), 0, s, p);
-  int rc0 = check_launch("block-sparse backward work-item kernel");
-  if (rc0 != SA_OK) return rc0;
   if (p.is_causal) {
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, true, 0>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
     hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<T, D, NW, true, 1>), dim3(p.n_work), dim3(NW * 64), 0, s, p);
@@ -1040,6 +1045,22 @@ inline size_t bwd_plan_bytes(int Z, int H, int H_kv, int N, int route_block, int
   const size_t items = wb / sizeof(int4);
   return wb + static_cast<size_t>(T) * sizeof(int4) + bwd_plan_tbias_bytes(Z, H, N, route_block, t_max) +
          items * bwd_chunk(route_block) * (sizeof(int2) + sizeof(float));
+}
+// Points p's plan fields into the plan buffer (layout of bwd_plan_bytes).
+inline void bwd_plan_layout(BwdParams& p, char* pl, int Z, int H, int H_kv, int N, int route_block, int t_max,
+                            bool soft_bias) {
+  const int BK = bwd_key_tile(route_block);
+  const long long T = static_cast<long long>(Z) * H_kv * ((N + BK - 1) / BK);
+  const size_t wb = bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max);
+  const size_t items = wb / sizeof(int4);
+  const size_t C = bwd_chunk(route_block);
+  char* tb = pl + wb + static_cast<size_t>(T) * sizeof(int4);
+  char* rec = tb + bwd_plan_tbias_bytes(Z, H, N, route_block, t_max);
+  p.work = reinterpret_cast<const int4*>(pl);
+  p.multi = reinterpret_cast<const int4*>(pl + wb);
+  p.t_bias = soft_bias ? reinterpret_cast<const float*>(tb) : nullptr;
+  p.ent_rh = reinterpret_cast<int2*>(rec);
+  p.ent_b = reinterpret_cast<float*>(rec + items * C * sizeof(int2));
 }
 
 template <typename T, int D>
@@ -1158,18 +1179,8 @@ extern "C" int sa_block_sparse_bwd(const void* q, const void* k, const void* v, 
       return fail(SA_EINVAL, "n_work / n_multi do not come from sa_block_sparse_bwd_plan");
     }
     if (n_multi > 0 && !dkv_partials) return fail(SA_EINVAL, "dkv_partials is NULL but the plan has split tiles");
-    const char* pl = static_cast<const char*>(plan);
-    const size_t wb = bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max_count);
-    p.work = reinterpret_cast<const int4*>(pl);
-    p.multi = reinterpret_cast<const int4*>(pl + wb);
-    p.t_bias = soft_bias ? reinterpret_cast<const float*>(pl + wb + static_cast<size_t>(T) * sizeof(int4)) : nullptr;
-    {
-      char* rec = const_cast<char*>(pl) + wb + static_cast<size_t>(T) * sizeof(int4) +
-                  bwd_plan_tbias_bytes(Z, H, N, route_block, t_max_count);
-      const size_t items = wb / sizeof(int4);
-      p.ent_rh = reinterpret_cast<int2*>(rec);
-      p.ent_b = reinterpret_cast<float*>(rec + items * bwd_chunk(route_block) * sizeof(int2));
-    }
+    bwd_plan_layout(p, const_cast<char*>(static_cast<const char*>(plan)), Z, H, H_kv, N, route_block, t_max_count,
+                    soft_bias != nullptr);
     p.key_tile = BK;
     p.partials = dkv_partials;
     p.n_work = n_work;
@@ -1226,14 +1237,24 @@ extern "C" int sa_block_sparse_bwd_plan(const int32_t* lists, const int32_t* cou
   const size_t wb = bwd_plan_work_bytes(Z, H, H_kv, N, route_block, t_max_count);
   const long long T = static_cast<long long>(Z) * H_kv * p.ktiles;
   if (T > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large");
+  bwd_plan_layout(p, pl, Z, H, H_kv, N, route_block, t_max_count, soft_bias != nullptr);
+  p.key_tile = BK;
   hipLaunchKernelGGL(bwd_plan_kernel, dim3(1), dim3(1024), 0, s, p, BK, reinterpret_cast<int4*>(pl),
                      reinterpret_cast<int4*>(pl + wb), plan_info);
   int rc = check_launch("block-sparse backward plan kernel");
-  if (rc != SA_OK || !soft_bias || max_count == 0 || t_max_count == 0) return rc;
-  const long long pairs = static_cast<long long>(Z) * H * p.NB * max_count;
-  const long long g = (pairs + 255) / 256;
-  if (g > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
-  hipLaunchKernelGGL(bwd_tbias_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, p,
-                     reinterpret_cast<float*>(pl + wb + static_cast<size_t>(T) * sizeof(int4)));
-  return check_launch("block-sparse backward soft-bias transpose kernel");
+  if (rc != SA_OK) return rc;
+  if (soft_bias && max_count > 0 && t_max_count > 0) {
+    const long long pairs = static_cast<long long>(Z) * H * p.NB * max_count;
+    const long long g = (pairs + 255) / 256;
+    if (g > 0x7fffffffLL) return fail(SA_EINVAL, "problem too large for one launch");
+    hipLaunchKernelGGL(bwd_tbias_kernel, dim3(static_cast<unsigned>(g)), dim3(256), 0, s, p,
+                       const_cast<float*>(p.t_bias));
+    rc = check_launch("block-sparse backward soft-bias transpose kernel");
+    if (rc != SA_OK) return rc;
+  }
+  // entries of each work item, up to the item count the plan kernel wrote
+  const long long items = static_cast<long long>(wb / sizeof(int4));
+  const unsigned g_items = static_cast<unsigned>(std::min<long long>((items + 3) / 4, 2048));
+  hipLaunchKernelGGL(bwd_items_kernel, dim3(g_items), dim3(256), 0, s, p, plan_info);
+  return check_launch("block-sparse backward work-item kernel");
 }
