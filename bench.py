@@ -535,6 +535,9 @@ def main():
 
         for _ in range(3):
             bwd()
+        # as for the prefill step: the first tens of milliseconds of continuous
+        # work run below steady clocks (the first 20 calls measured ~10% slower)
+        spin_up(bwd, args.spinup_ms, torch)
         bwd_ms = time_launches(bwd, max(20, args.steps // 5), torch)
         bwd_flop = 2.5 * flop_alg      # S, dP, dV, dK, dQ: five products of the forward's two
         result["backward"] = {
