@@ -314,8 +314,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdParams p) {
 //       bwd_items_kernel then resolves each item's entries.
 // ============================================================================
 constexpr int kBwdSeg = 256;        // dQ: list entries staged in LDS at a time
-constexpr int kChunkStages = 32;    // dK/dV: 32-row query stages per work item
-constexpr int kMaxChunk = 32;       // entries per work item (route_block 32)
+constexpr int kChunkStages = 64;    // dK/dV: 32-row query stages per work item
+constexpr int kMaxChunk = 64;       // entries per work item (route_block 32); one wave resolves them
 
 // Chunk c of row r of a stage tile is stored at position c ^ bsw(r). Row-major
 // operand reads (lanes 0..15 read rows 0..15, one 16-byte chunk each) and
@@ -1020,7 +1020,9 @@ int launch_bwd_mfma(BwdParams& p, int D, int phase, hipStream_t s) {
 
 // Keys per dK/dV work item and transposed entries per item.
 inline int bwd_key_tile(int route_block) { return route_block >= 128 ? 128 : route_block; }
-inline int bwd_chunk(int route_block) { return std::max(1, kChunkStages / std::max(1, route_block / 32)); }
+inline int bwd_chunk(int route_block) {
+  return std::min(kMaxChunk, std::max(1, kChunkStages / std::max(1, route_block / 32)));
+}
 
 // Plan buffer: work items (int4, at most one per key tile plus one per `chunk`
 // transposed entries), split tiles (int4, at most one per key tile), then the
