@@ -142,9 +142,12 @@ def check_grads(got, ref, rel=2e-2):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("H,Hkv,N,D,rb,causal,bias", [
     (2, 2, 1000, 128, 128, True, False),    # ragged tail
-    (4, 1, 2048, 128, 128, True, True),     # sink tile of 4 x 16 entries: 8 items
+    (4, 1, 2048, 128, 128, True, True),     # sink tile of 4 x 16 entries: 4 items of 16
+    (2, 2, 2176, 128, 128, True, False),    # 17 sink entries: items of 16 and 1
     (2, 2, 1536, 64, 64, False, True),      # two waves per workgroup
+    (4, 2, 2048, 64, 64, True, True),       # route block 64: sink tile of 2 x 32 entries, 2 items of 32
     (2, 1, 640, 32, 32, True, False),       # one wave per workgroup
+    (4, 1, 1024, 64, 32, True, False),      # route block 32: sink tile of 4 x 32 entries, 2 items of 64
     (2, 2, 2048, 128, 256, True, True),     # two key tiles per route block
     (3, 3, 777, 64, 128, False, False),
 ])
