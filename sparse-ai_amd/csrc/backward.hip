@@ -747,8 +747,8 @@ __device__ __forceinline__ void resolve_entry(const BwdParams& p, int4 item, int
   p.ent_b[slot] = p.t_bias ? p.t_bias[trow * p.t_max + u] : 0.f;
 }
 
-__global__ __launch_bounds__(256) void bwd_items_kernel(BwdParams p, const int32_t* info) {
-  const int n_items = info[0], e = threadIdx.x & 63;
+__global__ __launch_bounds__(256) void bwd_items_kernel(BwdParams p, const int32_t* info, int max_items) {
+  const int n_items = min(info[0], max_items), e = threadIdx.x & 63;
   for (int w = blockIdx.x * 4 + (threadIdx.x >> 6); w < n_items; w += gridDim.x * 4) {
     const int4 item = p.work[w];
     const int ne = max(0, min(item.w - item.y * p.chunk, p.chunk));
@@ -1257,6 +1257,7 @@ extern "C" int sa_block_sparse_bwd_plan(const int32_t* lists, const int32_t* cou
   // entries of each work item, up to the item count the plan kernel wrote
   const long long items = static_cast<long long>(wb / sizeof(int4));
   const unsigned g_items = static_cast<unsigned>(std::min<long long>((items + 3) / 4, 2048));
-  hipLaunchKernelGGL(bwd_items_kernel, dim3(g_items), dim3(256), 0, s, p, plan_info);
+  hipLaunchKernelGGL(bwd_items_kernel, dim3(g_items), dim3(256), 0, s, p, plan_info,
+                     static_cast<int>(std::min<long long>(items, 0x7fffffffLL)));
   return check_launch("block-sparse backward work-item kernel");
 }
